@@ -1,0 +1,175 @@
+/*
+ * phasekv_hip.h — C ABI of the MI355X (gfx950) PhaseKV Stage-B decode path.
+ *
+ * Plain pointers, sizes and a HIP stream handle (hipStream_t passed as void*);
+ * no PyTorch types.  Every entry point returns an int status (PK_OK on success),
+ * never throws or aborts across the ABI, and launches asynchronously on the
+ * given stream.  pk_last_error() returns a thread-local message for the most
+ * recent failure of the calling thread.
+ *
+ * Tensor conventions:
+ *   - fp16 / bf16 values are passed as uint16_t bit patterns.
+ *   - "packed" buffers are uint8 with the quantized axis moved last and
+ *     ceil(len / (8 / bits)) bytes per row, code j of byte k at bits
+ *     [j*bits, (j+1)*bits) (LSB first), zero codes in the tail byte.
+ *   - "scale"/"mins" buffers are fp16 [rows, ceil(len / group_size)].
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   see the comment above each entry point.
+ */
+#ifndef PHASEKV_HIP_H
+#define PHASEKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------- */
+#define PK_OK 0
+#define PK_ERR_INVALID (-1)     /* invalid argument: the Python side raises ValueError */
+#define PK_ERR_RUNTIME (-2)     /* HIP runtime / launch failure: RuntimeError */
+
+/* ---- dtypes of quantize_pack inputs ---------------------------------------- */
+#define PK_DTYPE_F16 0
+#define PK_DTYPE_BF16 1
+#define PK_DTYPE_F32 2
+
+/* ---- segment kinds of the decode work list --------------------------------- */
+#define PK_SEG_KIVI 0    /* K per-channel: packed [.., Hkv, hd, ceil(S/vpb)], meta [.., Hkv, hd, ceil(S/kgs)];
+                            V per-token:   packed [.., Hkv, S, ceil(hd/vpb)], meta [.., Hkv, S, ceil(hd/vgs)] */
+#define PK_SEG_TOKEN 1   /* K and V both per-token (legacy layout): like V above */
+#define PK_SEG_FP16 2    /* uncompressed fp16 K/V [.., Hkv, S, hd], token stride given, hd contiguous */
+
+#define PK_MAX_SEGMENTS_PER_LAUNCH 8
+#define PK_WORKSPACE_COUNTER_BYTES 65536   /* counters of pk_fused_decode, at offset 0 */
+
+/* Last error message of the calling thread ("" if none). */
+const char* pk_last_error(void);
+
+/* Library version string. */
+const char* pk_version(void);
+
+/* Device properties the planner uses.  Replaces _device_sm_count
+ * (src/phasekv/kernels/attention_triton.py:599-601). */
+int pk_device_info(int device, int* cu_count, int* lds_bytes_per_cu, int* wave_size,
+                   int* l2_bytes);
+
+/* ---- packing (src/phasekv/kernels/packing.py) ------------------------------- */
+
+/* pack_low_bits (packing.py:41-64): codes uint8 [rows, length] contiguous ->
+ * out uint8 [rows, ceil(length / vpb)].  bits in {2, 4, 8}. */
+int pk_pack_low_bits(const uint8_t* codes, int64_t rows, int64_t length, int bits,
+                     uint8_t* out, void* stream);
+
+/* unpack_low_bits (packing.py:67-79): packed uint8 [rows, packed_len] contiguous ->
+ * out uint8 [rows, length], length <= packed_len * vpb. */
+int pk_unpack_low_bits(const uint8_t* packed, int64_t rows, int64_t packed_len, int bits,
+                       int64_t length, uint8_t* out, void* stream);
+
+/* quantize_pack (packing.py:115-155).  x is any-strided (element strides) with
+ * ndim <= 8 dims of the given dtype; axis in [0, ndim); group_size already
+ * resolved by the caller to gs = min(group_size, len) (or len).  Outputs are
+ * contiguous in the moved layout: out_packed [rows, ceil(len/vpb)],
+ * out_scale/out_mins fp16 [rows, ceil(len/gs)], rows = prod(shape) / len in
+ * the original order of the remaining dims.  Bit-exact with the reference. */
+int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_t* shape,
+                     const int64_t* strides, int axis, int bits, int group_size,
+                     uint8_t* out_packed, uint16_t* out_scale, uint16_t* out_mins,
+                     void* stream);
+
+/* unpack_dequantize (packing.py:158-175): inverse of pk_quantize_pack.  Writes
+ * fp16 out contiguous in the ORIGINAL layout orig_shape (ndim <= 8), with
+ * n_groups = number of groups per row stored in scale/mins. */
+int pk_unpack_dequantize(const uint8_t* packed, const uint16_t* scale, const uint16_t* mins,
+                         int ndim, const int64_t* orig_shape, int axis, int bits,
+                         int group_size, int64_t n_groups, uint16_t* out, void* stream);
+
+/* ---- decode attention (src/phasekv/kernels/attention_triton.py) ------------- */
+
+/* One segment of the decode work list.  All element strides; the two innermost
+ * dims of packed / meta buffers are contiguous.  For PK_SEG_FP16 the K/V data
+ * pointers are fp16 and k_meta / v_meta strides are unused; tok_stride is the
+ * element stride between tokens (hd is contiguous). */
+typedef struct pk_segment {
+  int32_t kind;            /* PK_SEG_* */
+  int32_t length;          /* tokens in the segment (max over the batch) */
+  int32_t k_bits, v_bits;  /* 2/4/8 (ignored for FP16) */
+  int32_t k_group, v_group;/* group sizes as stored in PackedTensor.group_size */
+  int32_t splits;          /* requested splits (work items along the tokens), 0 = planner */
+  int32_t split_len;       /* tokens per split; with splits > 0 exactly `splits` splits of
+                              split_len tokens are launched (trailing ones may be empty, like
+                              attention_triton.py:227-240); 0 = split_len = ceil(len / splits) */
+  const int32_t* seq_lens; /* device [batch] valid tokens per row, or NULL (= length) */
+  const void* k_data; const uint16_t* k_scale; const uint16_t* k_mins;
+  const void* v_data; const uint16_t* v_scale; const uint16_t* v_mins;
+  int64_t k_data_bstride, k_data_hstride;
+  int64_t k_meta_bstride, k_meta_hstride;
+  int64_t v_data_bstride, v_data_hstride;
+  int64_t v_meta_bstride, v_meta_hstride;
+  int64_t tok_stride;      /* FP16 only */
+} pk_segment;
+
+/* One decode problem: q [batch, Hq, hd] fp16 (hd contiguous) against a list of
+ * segments of the same kv heads.  Query head h reads kv head h / (Hq / Hkv)
+ * (reference.py:61-69).  Scores use 1/sqrt(hd) (attention_triton.py:631). */
+typedef struct pk_decode_problem {
+  int32_t batch, num_q_heads, num_kv_heads, head_dim;
+  const uint16_t* q;
+  int64_t q_bstride, q_hstride;
+  const pk_segment* segments;  /* host array */
+  int32_t num_segments;
+  int32_t reserved;
+} pk_decode_problem;
+
+/* Bytes of split-K workspace pk_decode_partials needs for this problem
+ * (a fixed PK_WORKSPACE_COUNTER_BYTES counter region first, then the partials
+ * m, l [batch*Hq][splits] and acc [batch*Hq][splits][hd] fp32).  Replaces the torch.empty
+ * partial buffers of _kivi_layer_partial (attention_triton.py:624-626). */
+int pk_decode_workspace_size(const pk_decode_problem* p, size_t* bytes, int32_t* total_splits);
+
+/* Split-K partial pass over every segment in one launch per
+ * PK_MAX_SEGMENTS_PER_LAUNCH segments.  Replaces the per-segment
+ * _decode_attn_kivi_split_kernel launches of fused_phasekv_decode
+ * (attention_triton.py:514-596, 662-665), the legacy per-token kernels
+ * (attention_triton.py:24-92, 145-213) and the FP16 hot partial
+ * (attention_triton.py:285-297). */
+int pk_decode_partials(const pk_decode_problem* p, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* Log-sum-exp combine of the partials (attention_triton.py:257-266, 300-307).
+ * If out is non-NULL writes the normalized fp16 output [batch, Hq, hd]
+ * contiguous; if out_m/out_l/out_acc are non-NULL writes the unnormalized
+ * (m, l, acc) fp32 [batch*Hq], [batch*Hq], [batch*Hq, hd]. */
+int pk_decode_combine(const pk_decode_problem* p, const void* workspace, uint16_t* out,
+                      float* out_m, float* out_l, float* out_acc, void* stream);
+
+/* Partials + combine in one launch: the last workgroup of each (batch, kv head)
+ * merges the splits (no second launch).  The counter region at the start of
+ * the workspace must be zero when the call starts; every call leaves it at
+ * zero, so a freshly allocated workspace is zeroed once with
+ * pk_decode_workspace_init and can then be reused by any problem.  Calls that
+ * share a workspace must be ordered (same stream).  Same result as
+ * pk_decode_partials followed by pk_decode_combine(out). */
+int pk_fused_decode(const pk_decode_problem* p, void* workspace, size_t workspace_bytes,
+                    uint16_t* out, void* stream);
+
+/* Zero the counter region of a decode workspace (a fill kernel, not a memset).
+ * workspace_bytes must be >= PK_WORKSPACE_COUNTER_BYTES. */
+int pk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/* Merge n partials per row: m, l [rows, n] and acc [rows, n, hd] fp32 contiguous.
+ * Writes normalized fp16 out [rows, hd] (_merge_partials, attention_triton.py:300-307)
+ * or, when out is NULL, unnormalized (m, l, acc) (_reduce_splits,
+ * attention_triton.py:257-266). */
+int pk_merge_partials(const float* m, const float* l, const float* acc, int64_t rows,
+                      int32_t n, int32_t head_dim, uint16_t* out, float* out_m,
+                      float* out_l, float* out_acc, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PHASEKV_HIP_H */

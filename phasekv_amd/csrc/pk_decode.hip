@@ -1,0 +1,556 @@
+// Split-K mixed-precision decode attention over the PhaseKV tiers (gfx950).
+//
+// One launch covers a list of segments (packed KIVI prompt / prompt-extension /
+// cold segments, legacy per-token packed segments and the FP16 hot window).
+// Each workgroup owns one (batch row, kv head, head slab, token chunk) and
+// computes the softmax partial (m, l, acc) of every query head of its GQA group
+// from a single read of the chunk's K/V bytes.  A log-sum-exp combine merges the
+// partials of all chunks of all segments.
+//
+// Reference semantics (paths relative to the reference checkout):
+//   per-segment kernel    src/phasekv/kernels/attention_triton.py:514-596
+//   split reduce / merge  src/phasekv/kernels/attention_triton.py:257-266, 300-307
+//   FP16 hot partial      src/phasekv/kernels/attention_triton.py:285-297
+//   legacy per-token K/V  src/phasekv/kernels/attention_triton.py:24-92, 145-213
+//   entry point           src/phasekv/kernels/attention_triton.py:643-669
+#include "pk_common.h"
+#include "pk_decode.h"
+
+#include <math.h>
+
+#include <algorithm>
+#include <vector>
+
+namespace pk {
+
+// ---------------------------------------------------------------------------
+// tile loaders of the generic kernel: dequantize one (token, channel) element
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float kivi_k_elem(const SegDev& s, int64_t kd_off, int64_t km_off,
+                                             int tok, int d) {
+  const int vpb = 8 / s.kbits;
+  const int64_t row_bytes = (s.length + vpb - 1) / vpb;
+  const int64_t row_groups = (s.length + s.kgs - 1) / s.kgs;
+  const uint32_t byte = s.kd[kd_off + d * row_bytes + tok / vpb];
+  const uint32_t code = (byte >> ((tok % vpb) * s.kbits)) & ((1u << s.kbits) - 1u);
+  const int64_t g = d * row_groups + tok / s.kgs;
+  return static_cast<float>(code) * pk_h2f(s.ks[km_off + g]) + pk_h2f(s.km[km_off + g]);
+}
+
+// Per-token packed element (V of every packed segment, K of legacy segments).
+__device__ __forceinline__ float token_elem(const uint8_t* data, const uint16_t* sc,
+                                            const uint16_t* mn, int bits, int gs, int hd,
+                                            int64_t d_off, int64_t m_off, int tok, int d) {
+  const int vpb = 8 / bits;
+  const int row_bytes = (hd + vpb - 1) / vpb;
+  const int row_groups = (hd + gs - 1) / gs;
+  const uint32_t byte = data[d_off + (int64_t)tok * row_bytes + d / vpb];
+  const uint32_t code = (byte >> ((d % vpb) * bits)) & ((1u << bits) - 1u);
+  const int64_t g = (int64_t)tok * row_groups + d / gs;
+  return static_cast<float>(code) * pk_h2f(sc[m_off + g]) + pk_h2f(mn[m_off + g]);
+}
+
+// Whole-workgroup log-sum-exp merge of one output row's C partials.
+__device__ void combine_row(const float* __restrict__ m, const float* __restrict__ l,
+                            const float* __restrict__ acc, int C, int hd, int64_t row,
+                            uint16_t* out, float* om, float* ol, float* oacc, float* w_s,
+                            int w_cap, float* red_s) {
+  const int tid = threadIdx.x;
+  const int nt = blockDim.x;
+  const float* mr = m + row * C;
+  const float* lr = l + row * C;
+  const float* ar = acc + row * C * (int64_t)hd;
+  float mx = -INFINITY;
+  for (int c = tid; c < C; c += nt) mx = fmaxf(mx, mr[c]);
+  red_s[tid] = mx;
+  __syncthreads();
+  for (int s = nt / 2; s > 0; s >>= 1) {
+    if (tid < s) red_s[tid] = fmaxf(red_s[tid], red_s[tid + s]);
+    __syncthreads();
+  }
+  const float M = red_s[0];
+  __syncthreads();
+  float lsum = 0.f;
+  // accumulators for up to kCombineMaxHd / nt channels per thread
+  float a[kCombineMaxHd / kThreads];
+#pragma unroll
+  for (int i = 0; i < kCombineMaxHd / kThreads; ++i) a[i] = 0.f;
+  const int chunk = min(kCombineChunk, w_cap);
+  for (int c0 = 0; c0 < C; c0 += chunk) {
+    const int cn = min(chunk, C - c0);
+    for (int c = tid; c < cn; c += nt) {
+      const float mc = mr[c0 + c];
+      const float w = (mc == -INFINITY) ? 0.f : expf(mc - M);
+      w_s[c] = w;
+      lsum += w * lr[c0 + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kCombineMaxHd / kThreads; ++i) {
+      const int d = tid + i * nt;
+      if (d < hd) {
+        float s = a[i];
+        for (int c = 0; c < cn; ++c) s += w_s[c] * ar[(int64_t)(c0 + c) * hd + d];
+        a[i] = s;
+      }
+    }
+    __syncthreads();
+  }
+  red_s[tid] = lsum;
+  __syncthreads();
+  for (int s = nt / 2; s > 0; s >>= 1) {
+    if (tid < s) red_s[tid] += red_s[tid + s];
+    __syncthreads();
+  }
+  const float L = red_s[0];
+  __syncthreads();
+  if (out) {
+    const float inv = 1.0f / L;
+#pragma unroll
+    for (int i = 0; i < kCombineMaxHd / kThreads; ++i) {
+      const int d = tid + i * nt;
+      if (d < hd) out[row * hd + d] = pk_f2h(a[i] * inv);
+    }
+  }
+  if (om && tid == 0) { om[row] = M; ol[row] = L; }
+  if (oacc) {
+#pragma unroll
+    for (int i = 0; i < kCombineMaxHd / kThreads; ++i) {
+      const int d = tid + i * nt;
+      if (d < hd) oacc[row * hd + d] = a[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// generic partial kernel (any power-of-two hd <= 256, any bits / group sizes)
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads)
+decode_partials_generic(const DecodeParams p) {
+  extern __shared__ float lds[];
+  const int tid = threadIdx.x;
+  const int hd = p.hd;
+  const int T = p.tile;
+  const int HS = p.HS;
+  float* q_s = lds;                       // [HS][hd]
+  float* acc_s = q_s + HS * hd;           // [HS][hd]
+  float* k_s = acc_s + HS * hd;           // [T][hd+1]
+  float* v_s = k_s + T * (hd + 1);        // [T][hd+1]
+  float* p_s = v_s + T * (hd + 1);        // [HS][T]
+  float* m_s = p_s + HS * T;              // [HS]
+  float* l_s = m_s + HS;                  // [HS]
+  float* a_s = l_s + HS;                  // [HS]
+  __shared__ int sh_last;
+
+  const int b = blockIdx.z;
+  const int kvh = blockIdx.y / p.nslab;
+  const int slab = blockIdx.y - kvh * p.nslab;
+  const int h0 = kvh * p.G + slab * HS;
+  const int nh = min(HS, p.G - slab * HS);
+
+  int si = 0;
+  while (si + 1 < p.nseg && (int)blockIdx.x >= p.seg[si + 1].lbegin) ++si;
+  const SegDev& s = p.seg[si];
+  const int local = blockIdx.x - s.lbegin;
+  const int cg = s.gbegin + local;
+  int len_b = s.length;
+  if (s.seq_lens) len_b = min(len_b, s.seq_lens[b]);
+  const int t_begin = local * s.chunk_len;
+  const int t_end = min(t_begin + s.chunk_len, len_b);
+
+  for (int i = tid; i < nh * hd; i += kThreads) {
+    const int h = i / hd, d = i - h * hd;
+    q_s[i] = pk_h2f(p.q[b * p.q_bs + (int64_t)(h0 + h) * p.q_hs + d]);
+    acc_s[i] = 0.f;
+  }
+  for (int h = tid; h < nh; h += kThreads) { m_s[h] = -INFINITY; l_s[h] = 0.f; }
+
+  const int64_t kd_off = b * s.kd_bs + kvh * s.kd_hs;
+  const int64_t km_off = b * s.km_bs + kvh * s.km_hs;
+  const int64_t vd_off = b * s.vd_bs + kvh * s.vd_hs;
+  const int64_t vm_off = b * s.vm_bs + kvh * s.vm_hs;
+  __syncthreads();
+
+  for (int t0 = t_begin; t0 < t_end; t0 += T) {
+    const int nt = min(T, t_end - t0);
+    // ---- dequantize the K/V tile into LDS (fp32) ----
+    if (s.kind == PK_SEG_KIVI) {
+      for (int i = tid; i < T * hd; i += kThreads) {
+        const int d = i / T, t = i - d * T;          // tokens fastest: one channel row
+        k_s[t * (hd + 1) + d] = (t < nt) ? kivi_k_elem(s, kd_off, km_off, t0 + t, d) : 0.f;
+      }
+    } else if (s.kind == PK_SEG_TOKEN) {
+      for (int i = tid; i < T * hd; i += kThreads) {
+        const int t = i / hd, d = i - t * hd;
+        k_s[t * (hd + 1) + d] = (t < nt) ? token_elem(s.kd, s.ks, s.km, s.kbits, s.kgs, hd, kd_off,
+                                                      km_off, t0 + t, d) : 0.f;
+      }
+    } else {
+      const uint16_t* kh = reinterpret_cast<const uint16_t*>(s.kd);
+      for (int i = tid; i < T * hd; i += kThreads) {
+        const int t = i / hd, d = i - t * hd;
+        k_s[t * (hd + 1) + d] = (t < nt) ? pk_h2f(kh[kd_off + (int64_t)(t0 + t) * s.tok_stride + d]) : 0.f;
+      }
+    }
+    if (s.kind == PK_SEG_FP16) {
+      const uint16_t* vh = reinterpret_cast<const uint16_t*>(s.vd);
+      for (int i = tid; i < T * hd; i += kThreads) {
+        const int t = i / hd, d = i - t * hd;
+        v_s[t * (hd + 1) + d] = (t < nt) ? pk_h2f(vh[vd_off + (int64_t)(t0 + t) * s.tok_stride + d]) : 0.f;
+      }
+    } else {
+      for (int i = tid; i < T * hd; i += kThreads) {
+        const int t = i / hd, d = i - t * hd;
+        v_s[t * (hd + 1) + d] = (t < nt) ? token_elem(s.vd, s.vs, s.vm, s.vbits, s.vgs, hd, vd_off,
+                                                      vm_off, t0 + t, d) : 0.f;
+      }
+    }
+    __syncthreads();
+    // ---- scores ----
+    for (int i = tid; i < nh * T; i += kThreads) {
+      const int h = i / T, t = i - h * T;
+      float sc = -INFINITY;
+      if (t < nt) {
+        const float* qr = q_s + h * hd;
+        const float* kr = k_s + t * (hd + 1);
+        float dot = 0.f;
+        for (int d = 0; d < hd; ++d) dot += qr[d] * kr[d];
+        sc = dot * p.scale;
+      }
+      p_s[i] = sc;
+    }
+    __syncthreads();
+    // ---- online softmax (one thread per head) ----
+    for (int h = tid; h < nh; h += kThreads) {
+      float* pr = p_s + h * T;
+      float mt = -INFINITY;
+      for (int t = 0; t < nt; ++t) mt = fmaxf(mt, pr[t]);
+      const float m_old = m_s[h];
+      const float m_new = fmaxf(m_old, mt);
+      const float alpha = (m_old == -INFINITY) ? 0.f : __expf(m_old - m_new);
+      float sum = 0.f;
+      for (int t = 0; t < T; ++t) {
+        const float e = (t < nt) ? __expf(pr[t] - m_new) : 0.f;
+        pr[t] = e;
+        sum += e;
+      }
+      l_s[h] = l_s[h] * alpha + sum;
+      m_s[h] = m_new;
+      a_s[h] = alpha;
+    }
+    __syncthreads();
+    // ---- P V ----
+    for (int i = tid; i < nh * hd; i += kThreads) {
+      const int h = i / hd, d = i - h * hd;
+      const float* pr = p_s + h * T;
+      float a = acc_s[i] * a_s[h];
+      for (int t = 0; t < nt; ++t) a += pr[t] * v_s[t * (hd + 1) + d];
+      acc_s[i] = a;
+    }
+    __syncthreads();
+  }
+
+  // ---- write the partial of every head of the slab ----
+  for (int i = tid; i < nh * hd; i += kThreads) {
+    const int h = i / hd, d = i - h * hd;
+    const int64_t row = (int64_t)b * p.Hq + h0 + h;
+    p.ws_acc[(row * p.C + cg) * hd + d] = acc_s[i];
+  }
+  for (int h = tid; h < nh; h += kThreads) {
+    const int64_t row = (int64_t)b * p.Hq + h0 + h;
+    p.ws_m[row * p.C + cg] = m_s[h];
+    p.ws_l[row * p.C + cg] = l_s[h];
+  }
+  if (!p.fused) return;
+
+  // ---- fused combine: the last workgroup of this (b, kv head, slab) merges ----
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    unsigned* ctr = p.counters + ((int64_t)b * p.Hkv + kvh) * p.nslab + slab;
+    const unsigned prev = atomicAdd(ctr, 1u);
+    const int last = (prev == (unsigned)(p.C - 1));
+    if (last) atomicExch(ctr, 0u);   // leave the counter at zero for the next call
+    sh_last = last;
+  }
+  __syncthreads();
+  if (!sh_last) return;
+  __threadfence();
+  // LDS reuse: the tile buffers are free now.
+  float* w_s = k_s;
+  float* red_s = v_s;
+  for (int h = 0; h < nh; ++h) {
+    const int64_t row = (int64_t)b * p.Hq + h0 + h;
+    combine_row(p.ws_m, p.ws_l, p.ws_acc, p.C, hd, row, p.out, nullptr, nullptr, nullptr, w_s,
+                T * (hd + 1), red_s);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+combine_kernel(const float* __restrict__ m, const float* __restrict__ l,
+               const float* __restrict__ acc, int C, int hd, uint16_t* out, float* om, float* ol,
+               float* oacc) {
+  __shared__ float w_s[kCombineChunk];
+  __shared__ float red_s[kThreads];
+  combine_row(m, l, acc, C, hd, blockIdx.x, out, om, ol, oacc, w_s, kCombineChunk, red_s);
+}
+
+__global__ void zero_words_kernel(unsigned* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// host-side planning
+// ---------------------------------------------------------------------------
+static int validate_problem(const pk_decode_problem* p) {
+  if (!p) return fail("null problem");
+  if (p->batch <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0 || p->head_dim <= 0)
+    return fail("batch, heads and head_dim must be positive");
+  if (p->num_q_heads % p->num_kv_heads)
+    return fail("num_q_heads must be a multiple of num_kv_heads");
+  const int hd = p->head_dim;
+  if (hd & (hd - 1)) return fail("head_dim must be a power of two");
+  if (hd > kCombineMaxHd) return fail("head_dim above 256 is not supported");
+  if (!p->q) return fail("null q");
+  if (p->num_segments <= 0 || !p->segments) return fail("no segments to attend");
+  {
+    const int G = p->num_q_heads / p->num_kv_heads;
+    const int HS = std::min(G, std::max(1, 2048 / hd));
+    const int64_t counters = (int64_t)p->batch * p->num_kv_heads * cdiv(G, HS);
+    if (counters * (int64_t)sizeof(unsigned) > PK_WORKSPACE_COUNTER_BYTES)
+      return fail("batch * kv heads too large for the workspace counter region");
+  }
+  for (int i = 0; i < p->num_segments; ++i) {
+    const pk_segment& s = p->segments[i];
+    if (s.length <= 0) return fail("segment " + std::to_string(i) + " is empty");
+    if (!s.k_data || !s.v_data) return fail("segment " + std::to_string(i) + ": null K/V data");
+    if (s.splits < 0 || s.split_len < 0) return fail("splits and split_len must be non-negative");
+    if (s.split_len > 0 && (s.splits <= 0 || (int64_t)s.splits * s.split_len < s.length))
+      return fail("split_len needs splits with splits * split_len >= length");
+    if (s.kind == PK_SEG_FP16) {
+      if (s.tok_stride < hd) return fail("FP16 segment token stride below head_dim");
+      continue;
+    }
+    if (s.kind != PK_SEG_KIVI && s.kind != PK_SEG_TOKEN)
+      return fail("unknown segment kind " + std::to_string(s.kind));
+    if (!valid_bits(s.k_bits) || !valid_bits(s.v_bits)) return fail("bits must be one of (2, 4, 8)");
+    if (s.k_group <= 0 || s.v_group <= 0) return fail("group sizes must be positive");
+    if (!s.k_scale || !s.k_mins || !s.v_scale || !s.v_mins)
+      return fail("segment " + std::to_string(i) + ": null scale/min");
+    if (s.kind == PK_SEG_KIVI && s.k_group > s.length)
+      return fail("K group size exceeds the segment length");
+    if (s.v_group > hd) return fail("V group size exceeds head_dim");
+    if (s.kind == PK_SEG_TOKEN && s.k_group > hd) return fail("K group size exceeds head_dim");
+  }
+  return PK_OK;
+}
+
+struct Plan {
+  int G, HS, nslab, tile;
+  int C;
+  std::vector<int> n_chunks, chunk_len, gbegin;
+  size_t off_m, off_l, off_acc, bytes;
+};
+
+static Plan make_plan(const pk_decode_problem* p) {
+  Plan pl{};
+  const int hd = p->head_dim;
+  pl.G = p->num_q_heads / p->num_kv_heads;
+  pl.HS = std::min(pl.G, std::max(1, 2048 / hd));
+  pl.nslab = static_cast<int>(cdiv(pl.G, pl.HS));
+  pl.tile = std::min(64, std::max(8, 4096 / hd));
+  int64_t total_len = 0;
+  for (int i = 0; i < p->num_segments; ++i) total_len += p->segments[i].length;
+  const int64_t per_bh = (int64_t)p->batch * p->num_kv_heads * pl.nslab;
+  const int64_t want = 4LL * device_cu_count();
+  const int64_t chunks_target = std::max<int64_t>(1, cdiv(want, per_bh));
+  int64_t auto_len = cdiv(total_len, chunks_target);
+  auto_len = std::max<int64_t>(kMinChunk, cdiv(auto_len, kMinChunk) * kMinChunk);
+  pl.C = 0;
+  for (int i = 0; i < p->num_segments; ++i) {
+    const pk_segment& s = p->segments[i];
+    int64_t cl;
+    int64_t nc;
+    if (s.splits > 0 && s.split_len > 0) {
+      cl = s.split_len;
+      nc = s.splits;
+    } else if (s.splits > 0) {
+      cl = cdiv(s.length, std::min<int64_t>(s.length, s.splits));
+      nc = cdiv(s.length, cl);
+    } else {
+      cl = std::min<int64_t>(auto_len, s.length);
+      nc = cdiv(s.length, cl);
+    }
+    pl.chunk_len.push_back(static_cast<int>(cl));
+    pl.n_chunks.push_back(static_cast<int>(nc));
+    pl.gbegin.push_back(pl.C);
+    pl.C += static_cast<int>(nc);
+  }
+  const int64_t rows = (int64_t)p->batch * p->num_q_heads;
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  pl.off_m = PK_WORKSPACE_COUNTER_BYTES;
+  pl.off_l = align(pl.off_m + rows * pl.C * sizeof(float));
+  pl.off_acc = align(pl.off_l + rows * pl.C * sizeof(float));
+  pl.bytes = align(pl.off_acc + rows * pl.C * (size_t)hd * sizeof(float));
+  return pl;
+}
+
+static void fill_segment(SegDev& d, const pk_segment& s) {
+  d.kind = s.kind;
+  d.length = s.length;
+  d.kbits = s.k_bits;
+  d.vbits = s.v_bits;
+  d.kgs = s.k_group;
+  d.vgs = s.v_group;
+  d.seq_lens = s.seq_lens;
+  d.kd = static_cast<const uint8_t*>(s.k_data);
+  d.ks = s.k_scale;
+  d.km = s.k_mins;
+  d.vd = static_cast<const uint8_t*>(s.v_data);
+  d.vs = s.v_scale;
+  d.vm = s.v_mins;
+  d.kd_bs = s.k_data_bstride; d.kd_hs = s.k_data_hstride;
+  d.km_bs = s.k_meta_bstride; d.km_hs = s.k_meta_hstride;
+  d.vd_bs = s.v_data_bstride; d.vd_hs = s.v_data_hstride;
+  d.vm_bs = s.v_meta_bstride; d.vm_hs = s.v_meta_hstride;
+  d.tok_stride = s.tok_stride;
+}
+
+static size_t generic_lds_bytes(const Plan& pl, int hd) {
+  return sizeof(float) * ((size_t)2 * pl.HS * hd + (size_t)2 * pl.tile * (hd + 1) +
+                          (size_t)pl.HS * pl.tile + 3 * pl.HS);
+}
+
+static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws, bool fused,
+                           uint16_t* out, hipStream_t stream) {
+  DecodeParams dp{};
+  dp.B = p->batch;
+  dp.Hq = p->num_q_heads;
+  dp.Hkv = p->num_kv_heads;
+  dp.hd = p->head_dim;
+  dp.G = pl.G;
+  dp.HS = pl.HS;
+  dp.nslab = pl.nslab;
+  dp.tile = pl.tile;
+  dp.scale = 1.0f / sqrtf(static_cast<float>(p->head_dim));
+  dp.q = p->q;
+  dp.q_bs = p->q_bstride;
+  dp.q_hs = p->q_hstride;
+  dp.ws_m = reinterpret_cast<float*>(ws + pl.off_m);
+  dp.ws_l = reinterpret_cast<float*>(ws + pl.off_l);
+  dp.ws_acc = reinterpret_cast<float*>(ws + pl.off_acc);
+  dp.counters = reinterpret_cast<unsigned*>(ws);
+  dp.C = pl.C;
+  dp.fused = fused ? 1 : 0;
+  dp.out = out;
+  const size_t lds = generic_lds_bytes(pl, p->head_dim);
+  for (int first = 0; first < p->num_segments; first += kMaxSeg) {
+    const int n = std::min(kMaxSeg, p->num_segments - first);
+    int lchunks = 0;
+    for (int i = 0; i < n; ++i) {
+      SegDev& d = dp.seg[i];
+      fill_segment(d, p->segments[first + i]);
+      d.chunk_len = pl.chunk_len[first + i];
+      d.n_chunks = pl.n_chunks[first + i];
+      d.gbegin = pl.gbegin[first + i];
+      d.lbegin = lchunks;
+      lchunks += d.n_chunks;
+    }
+    dp.nseg = n;
+    dim3 grid(lchunks, p->num_kv_heads * pl.nslab, p->batch);
+    hipLaunchKernelGGL(decode_partials_generic, grid, dim3(kThreads), lds, stream, dp);
+    int rc = check_launch("decode_partials");
+    if (rc) return rc;
+  }
+  return PK_OK;
+}
+
+}  // namespace pk
+
+using namespace pk;
+
+extern "C" int pk_decode_workspace_size(const pk_decode_problem* p, size_t* bytes,
+                                        int32_t* total_splits) {
+  clear_error();
+  int rc = validate_problem(p);
+  if (rc) return rc;
+  Plan pl = make_plan(p);
+  if (bytes) *bytes = pl.bytes;
+  if (total_splits) *total_splits = pl.C;
+  return PK_OK;
+}
+
+extern "C" int pk_decode_partials(const pk_decode_problem* p, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = validate_problem(p);
+  if (rc) return rc;
+  Plan pl = make_plan(p);
+  if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
+  return launch_partials(p, pl, static_cast<char*>(workspace), false, nullptr,
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pk_decode_combine(const pk_decode_problem* p, const void* workspace,
+                                 uint16_t* out, float* out_m, float* out_l, float* out_acc,
+                                 void* stream) {
+  clear_error();
+  int rc = validate_problem(p);
+  if (rc) return rc;
+  if (!workspace) return fail("null workspace");
+  if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
+  Plan pl = make_plan(p);
+  const char* ws = static_cast<const char*>(workspace);
+  const int64_t rows = (int64_t)p->batch * p->num_q_heads;
+  hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const float*>(ws + pl.off_m),
+                     reinterpret_cast<const float*>(ws + pl.off_l),
+                     reinterpret_cast<const float*>(ws + pl.off_acc), pl.C, p->head_dim, out,
+                     out_m, out_l, out_acc);
+  return check_launch("decode_combine");
+}
+
+extern "C" int pk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (!workspace) return fail("null workspace");
+  if (workspace_bytes < PK_WORKSPACE_COUNTER_BYTES) return fail("workspace smaller than its counter region");
+  const int64_t words = PK_WORKSPACE_COUNTER_BYTES / 4;
+  hipLaunchKernelGGL(zero_words_kernel, dim3(cdiv(words, kThreads)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<unsigned*>(workspace), words);
+  return check_launch("decode_workspace_init");
+}
+
+extern "C" int pk_fused_decode(const pk_decode_problem* p, void* workspace, size_t workspace_bytes,
+                               uint16_t* out, void* stream) {
+  clear_error();
+  int rc = validate_problem(p);
+  if (rc) return rc;
+  if (!out) return fail("null output");
+  Plan pl = make_plan(p);
+  if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (p->num_segments <= kMaxSeg) {
+    return launch_partials(p, pl, static_cast<char*>(workspace), true, out, s);
+  }
+  rc = launch_partials(p, pl, static_cast<char*>(workspace), false, nullptr, s);
+  if (rc) return rc;
+  return pk_decode_combine(p, workspace, out, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int pk_merge_partials(const float* m, const float* l, const float* acc, int64_t rows,
+                                 int32_t n, int32_t head_dim, uint16_t* out, float* out_m,
+                                 float* out_l, float* out_acc, void* stream) {
+  clear_error();
+  if (rows < 0 || n <= 0 || head_dim <= 0) return fail("rows, n and head_dim must be positive");
+  if (head_dim > kCombineMaxHd) return fail("head_dim above 256 is not supported");
+  if (!m || !l || !acc) return fail("null partials");
+  if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
+  if (rows == 0) return PK_OK;
+  hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), m, l, acc, n, head_dim, out, out_m, out_l,
+                     out_acc);
+  return check_launch("merge_partials");
+}

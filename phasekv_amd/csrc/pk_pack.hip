@@ -1,0 +1,367 @@
+// Sub-byte pack/unpack and grouped min/max quantization kernels (gfx950).
+//
+// Semantics follow src/phasekv/kernels/packing.py of the reference:
+//   pack_low_bits      packing.py:41-64
+//   unpack_low_bits    packing.py:67-79
+//   quantize_pack      packing.py:115-155
+//   unpack_dequantize  packing.py:158-175
+// All float arithmetic is IEEE float32 with explicit round-to-nearest
+// intrinsics (no contraction, no fast reciprocal) so the outputs are
+// bit-identical to the reference run by torch.
+#include "pk_common.h"
+
+// No multiply-add contraction anywhere in this file: the reference multiplies
+// and adds in separate float32 operations.
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxDims = 8;
+
+// ---------------------------------------------------------------------------
+// pack / unpack of uint8 codes along the last axis
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads)
+pack_low_bits_kernel(const uint8_t* __restrict__ codes, int64_t rows, int64_t length,
+                     int bits, int64_t nbytes, uint8_t* __restrict__ out) {
+  const int vpb = 8 / bits;
+  const int64_t total = rows * nbytes;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / nbytes;
+    const int64_t j = i - r * nbytes;
+    const uint8_t* src = codes + r * length;
+    uint32_t acc = 0;
+    for (int k = 0; k < vpb; ++k) {
+      const int64_t pos = j * vpb + k;
+      if (pos < length) acc |= static_cast<uint32_t>(src[pos]) << (k * bits);
+    }
+    out[i] = static_cast<uint8_t>(acc);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+unpack_low_bits_kernel(const uint8_t* __restrict__ packed, int64_t rows, int64_t packed_len,
+                       int bits, int64_t length, uint8_t* __restrict__ out) {
+  const int vpb = 8 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  const int64_t total = rows * length;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / length;
+    const int64_t pos = i - r * length;
+    const uint32_t byte = packed[r * packed_len + pos / vpb];
+    out[i] = static_cast<uint8_t>((byte >> ((pos % vpb) * bits)) & mask);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// quantize_pack
+// ---------------------------------------------------------------------------
+struct QuantParams {
+  const void* x;
+  int dtype;
+  int npre;                       // number of non-axis dims
+  int64_t pre_size[kMaxDims];
+  int64_t pre_stride[kMaxDims];
+  int64_t ax_stride;
+  int64_t len;
+  int bits;
+  int gs;
+  int64_t ngroups;
+  int64_t nbytes;
+  int64_t rows;
+  int rows_fastest;               // thread index -> (row fastest) or (group fastest)
+  uint8_t* packed;
+  uint16_t* scale;
+  uint16_t* mins;
+};
+
+__device__ __forceinline__ int64_t row_offset(const QuantParams& p, int64_t r) {
+  int64_t off = 0;
+  for (int d = p.npre - 1; d >= 0; --d) {
+    const int64_t sz = p.pre_size[d];
+    const int64_t idx = r % sz;
+    r /= sz;
+    off += idx * p.pre_stride[d];
+  }
+  return off;
+}
+
+__device__ __forceinline__ float load_x(const QuantParams& p, int64_t off) {
+  if (p.dtype == PK_DTYPE_F16) return pk_h2f(static_cast<const uint16_t*>(p.x)[off]);
+  if (p.dtype == PK_DTYPE_BF16) return pk_bf2f(static_cast<const uint16_t*>(p.x)[off]);
+  return static_cast<const float*>(p.x)[off];
+}
+
+// min / max with NaN propagation (torch.amin / amax semantics).
+__device__ __forceinline__ float nan_min(float a, float b) { return (b < a || b != b) ? b : a; }
+__device__ __forceinline__ float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
+
+struct GroupStats {
+  float mn;
+  float scale;   // float32 scale used for the codes (the fp16 copy is what is stored)
+};
+
+// Statistics of group g of the row at base offset `off`.  The reference pads the
+// tail group with copies of the last element, which changes neither its min nor
+// its max, so only the real elements are scanned.
+__device__ __forceinline__ GroupStats group_stats(const QuantParams& p, int64_t off, int64_t g) {
+  const int64_t begin = g * p.gs;
+  const int64_t end = min(begin + p.gs, p.len);
+  float mn = load_x(p, off + begin * p.ax_stride);
+  float mx = mn;
+  for (int64_t i = begin + 1; i < end; ++i) {
+    const float v = load_x(p, off + i * p.ax_stride);
+    mn = nan_min(mn, v);
+    mx = nan_max(mx, v);
+  }
+  float range = __fsub_rn(mx, mn);
+  range = (range < 1e-8f) ? 1e-8f : range;           // clamp_(min=1e-8), NaN kept
+  const float qmax = static_cast<float>((1 << p.bits) - 1);
+  return GroupStats{mn, __fdiv_rn(range, qmax)};
+}
+
+__device__ __forceinline__ uint32_t quant_code(float v, const GroupStats& s, int bits) {
+  const float qmax = static_cast<float>((1 << bits) - 1);
+  float q = rintf(__fdiv_rn(__fsub_rn(v, s.mn), s.scale));   // round half to even
+  q = fminf(fmaxf(q, 0.0f), qmax);
+  return static_cast<uint32_t>(q);
+}
+
+// One thread per (row, group) when whole groups cover whole bytes (gs % vpb == 0).
+__global__ void __launch_bounds__(kThreads)
+quantize_groups_kernel(QuantParams p) {
+  const int vpb = 8 / p.bits;
+  const int64_t total = p.rows * p.ngroups;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r, g;
+    if (p.rows_fastest) { g = i / p.rows; r = i - g * p.rows; }
+    else { r = i / p.ngroups; g = i - r * p.ngroups; }
+    const int64_t off = row_offset(p, r);
+    const GroupStats s = group_stats(p, off, g);
+    p.scale[r * p.ngroups + g] = pk_f2h(s.scale);
+    p.mins[r * p.ngroups + g] = pk_f2h(s.mn);
+    const int64_t begin = g * p.gs;
+    const int64_t end = min(begin + p.gs, p.len);
+    uint8_t* dst = p.packed + r * p.nbytes;
+    for (int64_t b0 = begin; b0 < end; b0 += vpb) {
+      uint32_t byte = 0;
+      for (int k = 0; k < vpb; ++k) {
+        const int64_t pos = b0 + k;
+        if (pos < end) byte |= quant_code(load_x(p, off + pos * p.ax_stride), s, p.bits) << (k * p.bits);
+      }
+      dst[b0 / vpb] = static_cast<uint8_t>(byte);
+    }
+  }
+}
+
+// General group sizes: metadata per (row, group) ...
+__global__ void __launch_bounds__(kThreads)
+quantize_meta_kernel(QuantParams p) {
+  const int64_t total = p.rows * p.ngroups;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / p.ngroups;
+    const int64_t g = i - r * p.ngroups;
+    const GroupStats s = group_stats(p, row_offset(p, r), g);
+    p.scale[i] = pk_f2h(s.scale);
+    p.mins[i] = pk_f2h(s.mn);
+  }
+}
+
+// ... and codes per (row, output byte); a byte may straddle groups.
+__global__ void __launch_bounds__(kThreads)
+quantize_bytes_kernel(QuantParams p) {
+  const int vpb = 8 / p.bits;
+  const int64_t total = p.rows * p.nbytes;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / p.nbytes;
+    const int64_t j = i - r * p.nbytes;
+    const int64_t off = row_offset(p, r);
+    uint32_t byte = 0;
+    int64_t cur_g = -1;
+    GroupStats s{0.f, 1.f};
+    for (int k = 0; k < vpb; ++k) {
+      const int64_t pos = j * vpb + k;
+      if (pos >= p.len) break;
+      const int64_t g = pos / p.gs;
+      if (g != cur_g) { s = group_stats(p, off, g); cur_g = g; }
+      byte |= quant_code(load_x(p, off + pos * p.ax_stride), s, p.bits) << (k * p.bits);
+    }
+    p.packed[i] = static_cast<uint8_t>(byte);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// unpack_dequantize: one thread per output element in the original layout
+// ---------------------------------------------------------------------------
+struct DequantParams {
+  const uint8_t* packed;
+  const uint16_t* scale;
+  const uint16_t* mins;
+  int ndim;
+  int axis;
+  int64_t shape[kMaxDims];
+  int64_t len;
+  int64_t nbytes;
+  int64_t ngroups;
+  int bits;
+  int gs;
+  int64_t total;
+  uint16_t* out;
+};
+
+__global__ void __launch_bounds__(kThreads)
+unpack_dequantize_kernel(DequantParams p) {
+  const int vpb = 8 / p.bits;
+  const uint32_t mask = (1u << p.bits) - 1u;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < p.total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    int64_t rem = e, r = 0, rmul = 1, j = 0;
+    for (int d = p.ndim - 1; d >= 0; --d) {
+      const int64_t idx = rem % p.shape[d];
+      rem /= p.shape[d];
+      if (d == p.axis) { j = idx; }
+      else { r += idx * rmul; rmul *= p.shape[d]; }
+    }
+    const uint32_t byte = p.packed[r * p.nbytes + j / vpb];
+    const float code = static_cast<float>((byte >> ((j % vpb) * p.bits)) & mask);
+    const int64_t g = j / p.gs;
+    const float sc = pk_h2f(p.scale[r * p.ngroups + g]);
+    const float mn = pk_h2f(p.mins[r * p.ngroups + g]);
+    p.out[e] = pk_f2h(__fadd_rn(__fmul_rn(code, sc), mn));
+  }
+}
+
+inline int grid_for(int64_t total) {
+  const int64_t blocks = pk::cdiv(total, kThreads);
+  const int64_t cap = static_cast<int64_t>(pk::device_cu_count()) * 32;
+  return static_cast<int>(blocks < cap ? (blocks > 0 ? blocks : 1) : cap);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C entry points
+// ---------------------------------------------------------------------------
+extern "C" int pk_pack_low_bits(const uint8_t* codes, int64_t rows, int64_t length, int bits,
+                                uint8_t* out, void* stream) {
+  pk::clear_error();
+  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+  if (rows < 0 || length < 0) return pk::fail("rows and length must be non-negative");
+  const int64_t nbytes = pk::cdiv(length, 8 / bits);
+  if (rows * nbytes == 0) return PK_OK;
+  if (!codes || !out) return pk::fail("null pointer");
+  hipLaunchKernelGGL(pack_low_bits_kernel, dim3(grid_for(rows * nbytes)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), codes, rows, length, bits, nbytes, out);
+  return pk::check_launch("pack_low_bits");
+}
+
+extern "C" int pk_unpack_low_bits(const uint8_t* packed, int64_t rows, int64_t packed_len,
+                                  int bits, int64_t length, uint8_t* out, void* stream) {
+  pk::clear_error();
+  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+  if (rows < 0 || length < 0 || packed_len < 0) return pk::fail("sizes must be non-negative");
+  if (length > packed_len * (8 / bits)) return pk::fail("length exceeds the packed codes");
+  if (rows * length == 0) return PK_OK;
+  if (!packed || !out) return pk::fail("null pointer");
+  hipLaunchKernelGGL(unpack_low_bits_kernel, dim3(grid_for(rows * length)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), packed, rows, packed_len, bits, length, out);
+  return pk::check_launch("unpack_low_bits");
+}
+
+extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_t* shape,
+                                const int64_t* strides, int axis, int bits, int group_size,
+                                uint8_t* out_packed, uint16_t* out_scale, uint16_t* out_mins,
+                                void* stream) {
+  pk::clear_error();
+  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+  if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16 && dtype != PK_DTYPE_F32)
+    return pk::fail("x must be float16, bfloat16 or float32");
+  if (ndim < 1 || ndim > kMaxDims) return pk::fail("x must have 1..8 dims");
+  if (axis < 0 || axis >= ndim) return pk::fail("axis out of range");
+  QuantParams p{};
+  p.x = x;
+  p.dtype = dtype;
+  p.len = shape[axis];
+  p.ax_stride = strides[axis];
+  p.rows = 1;
+  int n = 0;
+  for (int d = 0; d < ndim; ++d) {
+    if (shape[d] < 0) return pk::fail("negative dimension");
+    if (d == axis) continue;
+    p.pre_size[n] = shape[d];
+    p.pre_stride[n] = strides[d];
+    p.rows *= shape[d];
+    ++n;
+  }
+  p.npre = n;
+  if (p.len <= 0 || p.rows == 0) {
+    if (p.len <= 0) return pk::fail("quantized axis must be non-empty");
+    return PK_OK;
+  }
+  if (group_size <= 0 || group_size > p.len) return pk::fail("group_size must be in [1, len]");
+  if (!x || !out_packed || !out_scale || !out_mins) return pk::fail("null pointer");
+  p.bits = bits;
+  p.gs = group_size;
+  p.ngroups = pk::cdiv(p.len, group_size);
+  p.nbytes = pk::cdiv(p.len, 8 / bits);
+  // Threads walk adjacent rows when the quantized axis is not the contiguous one,
+  // so neighbouring lanes read neighbouring addresses.
+  p.rows_fastest = (p.ax_stride != 1) ? 1 : 0;
+  p.packed = out_packed;
+  p.scale = out_scale;
+  p.mins = out_mins;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (group_size % (8 / bits) == 0) {
+    hipLaunchKernelGGL(quantize_groups_kernel, dim3(grid_for(p.rows * p.ngroups)),
+                       dim3(kThreads), 0, s, p);
+  } else {
+    hipLaunchKernelGGL(quantize_meta_kernel, dim3(grid_for(p.rows * p.ngroups)), dim3(kThreads),
+                       0, s, p);
+    int rc = pk::check_launch("quantize_pack(meta)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(quantize_bytes_kernel, dim3(grid_for(p.rows * p.nbytes)), dim3(kThreads),
+                       0, s, p);
+  }
+  return pk::check_launch("quantize_pack");
+}
+
+extern "C" int pk_unpack_dequantize(const uint8_t* packed, const uint16_t* scale,
+                                    const uint16_t* mins, int ndim, const int64_t* orig_shape,
+                                    int axis, int bits, int group_size, int64_t n_groups,
+                                    uint16_t* out, void* stream) {
+  pk::clear_error();
+  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+  if (ndim < 1 || ndim > kMaxDims) return pk::fail("orig_shape must have 1..8 dims");
+  if (axis < 0 || axis >= ndim) return pk::fail("axis out of range");
+  DequantParams p{};
+  p.ndim = ndim;
+  p.axis = axis;
+  p.total = 1;
+  for (int d = 0; d < ndim; ++d) {
+    if (orig_shape[d] < 0) return pk::fail("negative dimension");
+    p.shape[d] = orig_shape[d];
+    p.total *= orig_shape[d];
+  }
+  p.len = orig_shape[axis];
+  if (p.total == 0) return PK_OK;
+  if (group_size <= 0) return pk::fail("group_size must be positive");
+  if (n_groups * group_size < p.len) return pk::fail("scale/mins hold fewer groups than the axis needs");
+  if (!packed || !scale || !mins || !out) return pk::fail("null pointer");
+  p.packed = packed;
+  p.scale = scale;
+  p.mins = mins;
+  p.bits = bits;
+  p.gs = group_size;
+  p.ngroups = n_groups;
+  p.nbytes = pk::cdiv(p.len, 8 / bits);
+  p.out = out;
+  hipLaunchKernelGGL(unpack_dequantize_kernel, dim3(grid_for(p.total)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return pk::check_launch("unpack_dequantize");
+}

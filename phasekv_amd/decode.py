@@ -1,0 +1,267 @@
+"""Host side of the decode path: tensors -> C-ABI segment descriptors -> HIP launches.
+
+The drop-in ``kernels.attention_triton`` module and the bench build their calls
+from these helpers.  Segment kinds:
+
+* KIVI  — a ``PackedKVSegment`` of the cache: K packed per channel along tokens
+  (``quantize_pack(K, bits, axis=-2)``), V packed per token along head_dim
+  (``axis=-1``), ``src/phasekv/phasekv_cache.py:101-107``.
+* TOKEN — legacy layout, K and V both packed per token
+  (``scripts/bench_decode_kernel.py:82-83`` of the reference).
+* FP16  — uncompressed fp16 K/V, e.g. the hot window views
+  (``src/phasekv/phasekv_cache.py:75-79``), which are strided over the buffer
+  capacity and are read in place.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+
+def _inner_contiguous(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` if its two innermost dims are dense, else a contiguous copy."""
+    if t.dim() >= 2 and t.stride(-1) == 1 and (t.shape[-2] <= 1 or t.stride(-2) == t.shape[-1]):
+        return t
+    if t.dim() == 1 and t.stride(-1) == 1:
+        return t
+    return t.contiguous()
+
+
+def _bh_strides(t: torch.Tensor, batched: bool) -> Tuple[int, int]:
+    """(batch stride, head stride) in elements of a [B, H, ...] or [H, ...] tensor."""
+    if batched:
+        return t.stride(0), t.stride(1)
+    return 0, t.stride(0)
+
+
+class Segment:
+    """One C-ABI segment plus the tensors it points to (kept alive by this object)."""
+
+    def __init__(self, desc: _lib.PkSegment, keep: Sequence[torch.Tensor], length: int,
+                 num_kv_heads: int, head_dim: int, batch: int, device: torch.device):
+        self.desc = desc
+        self.keep = list(keep)
+        self.length = length
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.batch = batch
+        self.device = device
+
+
+def packed_segment(key, value, *, batched: bool, splits: int = 0, split_len: int = 0,
+                   seq_lens: Optional[torch.Tensor] = None) -> Segment:
+    """Segment from a K/V pair of ``PackedTensor`` (KIVI or legacy per-token layout).
+
+    ``batched``: orig_shape is [B, Hkv, S, hd] (else [Hkv, S, hd]).
+    """
+    nd = 4 if batched else 3
+    if len(key.orig_shape) != nd or tuple(value.orig_shape) != tuple(key.orig_shape):
+        raise ValueError("packed K/V must share one [B, Hkv, S, hd] (or [Hkv, S, hd]) shape")
+    tok_axis, dim_axis = nd - 2, nd - 1
+    if value.axis != dim_axis:
+        raise ValueError("V must be packed along head_dim (per token)")
+    if key.axis == tok_axis:
+        kind = _lib.PK_SEG_KIVI
+    elif key.axis == dim_axis:
+        kind = _lib.PK_SEG_TOKEN
+    else:
+        raise ValueError("K must be packed along tokens (KIVI) or head_dim (per token)")
+    shape = tuple(key.orig_shape)
+    batch = shape[0] if batched else 1
+    hkv, s_len, hd = shape[-3], shape[-2], shape[-1]
+    if s_len <= 0:
+        raise ValueError("packed K/V segment is empty")
+    dev = _lib.require_device(key.packed, key.scale, key.mins, value.packed, value.scale,
+                              value.mins)
+    kp, ks, km = (_inner_contiguous(t) for t in (key.packed, key.scale, key.mins))
+    vp, vs, vm = (_inner_contiguous(t) for t in (value.packed, value.scale, value.mins))
+    if ks.stride() != km.stride() or vs.stride() != vm.stride():
+        ks, km, vs, vm = ks.contiguous(), km.contiguous(), vs.contiguous(), vm.contiguous()
+    d = _lib.PkSegment()
+    d.kind = kind
+    d.length = s_len
+    d.k_bits, d.v_bits = key.bits, value.bits
+    d.k_group, d.v_group = key.group_size, value.group_size
+    d.splits, d.split_len = int(splits), int(split_len)
+    d.seq_lens = 0 if seq_lens is None else seq_lens.data_ptr()
+    d.k_data, d.k_scale, d.k_mins = kp.data_ptr(), ks.data_ptr(), km.data_ptr()
+    d.v_data, d.v_scale, d.v_mins = vp.data_ptr(), vs.data_ptr(), vm.data_ptr()
+    d.k_data_bstride, d.k_data_hstride = _bh_strides(kp, batched)
+    d.k_meta_bstride, d.k_meta_hstride = _bh_strides(ks, batched)
+    d.v_data_bstride, d.v_data_hstride = _bh_strides(vp, batched)
+    d.v_meta_bstride, d.v_meta_hstride = _bh_strides(vs, batched)
+    d.tok_stride = 0
+    keep = [kp, ks, km, vp, vs, vm] + ([seq_lens] if seq_lens is not None else [])
+    return Segment(d, keep, s_len, hkv, hd, batch, dev)
+
+
+def fp16_segment(k: torch.Tensor, v: torch.Tensor, *, batched: bool, splits: int = 0,
+                 split_len: int = 0, seq_lens: Optional[torch.Tensor] = None) -> Segment:
+    """Segment over uncompressed fp16 K/V [B, Hkv, S, hd] (or [Hkv, S, hd]), read in place."""
+    nd = 4 if batched else 3
+    if k.dim() != nd or k.shape != v.shape:
+        raise ValueError("fp16 K/V must share one [B, Hkv, S, hd] (or [Hkv, S, hd]) shape")
+    if k.dtype != torch.float16 or v.dtype != torch.float16:
+        raise ValueError("hot K/V must be float16")
+    dev = _lib.require_device(k, v)
+    if k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride() != v.stride():
+        k, v = k.contiguous(), v.contiguous()
+    batch = k.shape[0] if batched else 1
+    hkv, s_len, hd = k.shape[-3], k.shape[-2], k.shape[-1]
+    if s_len <= 0:
+        raise ValueError("fp16 segment is empty")
+    d = _lib.PkSegment()
+    d.kind = _lib.PK_SEG_FP16
+    d.length = s_len
+    d.splits, d.split_len = int(splits), int(split_len)
+    d.seq_lens = 0 if seq_lens is None else seq_lens.data_ptr()
+    d.k_data, d.v_data = k.data_ptr(), v.data_ptr()
+    d.k_data_bstride, d.k_data_hstride = _bh_strides(k, batched)
+    d.v_data_bstride, d.v_data_hstride = _bh_strides(v, batched)
+    d.tok_stride = k.stride(-2)
+    keep = [k, v] + ([seq_lens] if seq_lens is not None else [])
+    return Segment(d, keep, s_len, hkv, hd, batch, dev)
+
+
+class Problem:
+    """A decode problem (q plus segments) as the C structure, with its keep-alive list."""
+
+    def __init__(self, q: torch.Tensor, segments: List[Segment], num_attention_heads: int):
+        if not segments:
+            raise ValueError("no KV to attend: every tier is empty")
+        if q.dim() == 2:
+            q = q.unsqueeze(0)
+        if q.dim() != 3:
+            raise ValueError("query must be [Hq, hd] or [B, Hq, hd]")
+        if q.dtype != torch.float16:
+            raise ValueError("query must be float16")
+        batch, hq, hd = q.shape
+        if hq != num_attention_heads:
+            raise ValueError(f"query has {hq} heads, expected {num_attention_heads}")
+        dev = _lib.require_device(q, *[t for s in segments for t in s.keep])
+        hkv = segments[0].num_kv_heads
+        for s in segments:
+            if s.num_kv_heads != hkv or s.head_dim != hd:
+                raise ValueError("segments must share kv heads and head_dim with the query")
+            if s.batch != batch:
+                raise ValueError("segments and query must share the batch size")
+        if hq % hkv:
+            raise ValueError(f"Hq {hq} must be a multiple of Hkv {hkv}")
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        self.q = q
+        self.segments = segments
+        self.device = dev
+        self.batch, self.hq, self.hkv, self.hd = batch, hq, hkv, hd
+        arr = (_lib.PkSegment * len(segments))(*[s.desc for s in segments])
+        self._arr = arr
+        p = _lib.PkDecodeProblem()
+        p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim = batch, hq, hkv, hd
+        p.q = q.data_ptr()
+        p.q_bstride, p.q_hstride = q.stride(0), q.stride(1)
+        p.segments = ctypes.cast(arr, ctypes.POINTER(_lib.PkSegment))
+        p.num_segments = len(segments)
+        self.c = p
+
+    def workspace_size(self) -> Tuple[int, int]:
+        lib = _lib.load()
+        nbytes = ctypes.c_size_t(0)
+        splits = ctypes.c_int32(0)
+        _lib.check(lib.pk_decode_workspace_size(ctypes.byref(self.c), ctypes.byref(nbytes),
+                                                ctypes.byref(splits)), "decode_workspace_size")
+        return nbytes.value, splits.value
+
+
+# Reusable workspaces per (device, stream): calls on one stream are ordered, so
+# they can share one buffer; its counter region is zeroed once when allocated.
+_WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def cached_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    stream = _lib.stream_ptr(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes + nbytes // 2, 4 << 20)
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
+        _lib.check(_lib.load().pk_decode_workspace_init(ws.data_ptr(), ws.numel(), stream),
+                   "decode_workspace_init")
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def fused_decode(problem: Problem) -> torch.Tensor:
+    """Normalized attention output [B, Hq, hd] fp16 in one launch (per 8 segments)."""
+    nbytes, _ = problem.workspace_size()
+    ws = cached_workspace(problem.device, nbytes)
+    out = torch.empty(problem.batch, problem.hq, problem.hd, dtype=torch.float16,
+                      device=problem.device)
+    lib = _lib.load()
+    _lib.check(lib.pk_fused_decode(ctypes.byref(problem.c), ws.data_ptr(), ws.numel(),
+                                   out.data_ptr(), _lib.stream_ptr(problem.device)),
+               "fused_decode")
+    return out
+
+
+def decode_partials(problem: Problem):
+    """Raw split partials: (pm [B*Hq, C], pl [B*Hq, C], pacc [B*Hq, C, hd]) in a fresh buffer."""
+    nbytes, splits = problem.workspace_size()
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=problem.device)
+    lib = _lib.load()
+    _lib.check(lib.pk_decode_partials(ctypes.byref(problem.c), ws.data_ptr(), ws.numel(),
+                                      _lib.stream_ptr(problem.device)), "decode_partials")
+    rows = problem.batch * problem.hq
+    off_m = _lib.PK_WORKSPACE_COUNTER_BYTES
+    align = lambda x: (x + 255) & ~255
+    off_l = align(off_m + rows * splits * 4)
+    off_acc = align(off_l + rows * splits * 4)
+    pm = ws[off_m:off_m + rows * splits * 4].view(torch.float32).view(rows, splits)
+    pl = ws[off_l:off_l + rows * splits * 4].view(torch.float32).view(rows, splits)
+    pacc = ws[off_acc:off_acc + rows * splits * problem.hd * 4].view(torch.float32)
+    return pm, pl, pacc.view(rows, splits, problem.hd)
+
+
+def decode_mlacc(problem: Problem):
+    """Merged but unnormalized (m [B*Hq], l [B*Hq], acc [B*Hq, hd]) fp32."""
+    nbytes, _ = problem.workspace_size()
+    ws = cached_workspace(problem.device, nbytes)
+    rows = problem.batch * problem.hq
+    m = torch.empty(rows, dtype=torch.float32, device=problem.device)
+    l = torch.empty(rows, dtype=torch.float32, device=problem.device)
+    acc = torch.empty(rows, problem.hd, dtype=torch.float32, device=problem.device)
+    lib = _lib.load()
+    stream = _lib.stream_ptr(problem.device)
+    _lib.check(lib.pk_decode_partials(ctypes.byref(problem.c), ws.data_ptr(), ws.numel(), stream),
+               "decode_partials")
+    _lib.check(lib.pk_decode_combine(ctypes.byref(problem.c), ws.data_ptr(), None, m.data_ptr(),
+                                     l.data_ptr(), acc.data_ptr(), stream), "decode_combine")
+    return m, l, acc
+
+
+def merge_partials(m: torch.Tensor, l: torch.Tensor, acc: torch.Tensor, normalize: bool):
+    """Log-sum-exp merge over dim 1 of m, l [rows, n] and acc [rows, n, hd] (fp32)."""
+    dev = _lib.require_device(m, l, acc)
+    m = m.float().contiguous()
+    l = l.float().contiguous()
+    acc = acc.float().contiguous()
+    rows, n = m.shape
+    hd = acc.shape[-1]
+    lib = _lib.load()
+    stream = _lib.stream_ptr(dev)
+    if normalize:
+        out = torch.empty(rows, hd, dtype=torch.float16, device=dev)
+        _lib.check(lib.pk_merge_partials(m.data_ptr(), l.data_ptr(), acc.data_ptr(), rows, n, hd,
+                                         out.data_ptr(), None, None, None, stream),
+                   "merge_partials")
+        return out
+    om = torch.empty(rows, dtype=torch.float32, device=dev)
+    ol = torch.empty(rows, dtype=torch.float32, device=dev)
+    oacc = torch.empty(rows, hd, dtype=torch.float32, device=dev)
+    _lib.check(lib.pk_merge_partials(m.data_ptr(), l.data_ptr(), acc.data_ptr(), rows, n, hd,
+                                     None, om.data_ptr(), ol.data_ptr(), oacc.data_ptr(), stream),
+               "merge_partials")
+    return om, ol, oacc

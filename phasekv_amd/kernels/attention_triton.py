@@ -1,0 +1,264 @@
+"""Fused mixed-precision decode attention on MI355X (drop-in for the reference's attention_triton.py).
+
+The module keeps the reference's name and public functions so callers
+(``phasekv_cache``, the Qwen2 / Llama adapters, benches and tests) run
+unchanged, but nothing here is Triton: every function launches the
+hand-written HIP kernels of ``libphasekv_hip.so`` through its C ABI.
+
+Differences in *how*, not *what*:
+
+* ``fused_phasekv_decode`` covers the prompt segment, every prompt extension,
+  every cold segment and the FP16 hot window in ONE launch (per 8 segments):
+  split partials are merged by the last workgroup of each kv head, instead of
+  one Triton launch per segment plus ~25 torch ops
+  (``attention_triton.py:643-669``).
+* One workgroup serves all query heads of a GQA group, so each packed K/V byte
+  is read once per kv head, not once per query head (``attention_triton.py:534``).
+* ``num_splits`` / ``block_n`` / ``num_warps`` are validated exactly as the
+  reference's ``plan_kivi_decode`` does; when any is given, the split
+  boundaries follow that plan, otherwise the library's MI355X planner chooses.
+  ``num_warps`` has no other effect (workgroups are 256 threads).
+"""
+from __future__ import annotations
+
+from dataclasses import replace
+from functools import lru_cache
+
+import torch
+
+from .. import _lib
+from .. import decode as _dec
+from .launch_config import plan_kivi_decode
+from .packing import PackedTensor, _vals_per_byte
+
+
+@lru_cache(maxsize=32)
+def _device_sm_count(device: torch.device) -> int:
+    """Compute units of the device (``attention_triton.py:599-601``)."""
+    return _lib.device_cu_count(device)
+
+
+def _override_plan(seq_len, num_heads, head_dim, device, num_splits, block_n, num_warps):
+    """(splits, split_len) for a segment: the reference plan if any override is given."""
+    if num_splits is None and block_n is None and num_warps is None:
+        return 0, 0
+    cfg = plan_kivi_decode(seq_len, num_heads, head_dim, _device_sm_count(device),
+                           num_splits, block_n, num_warps)
+    return cfg.num_splits, cfg.split_len
+
+
+# ---------------------------------------------------------------------------
+# legacy per-token packed path (attention_triton.py:24-282)
+# ---------------------------------------------------------------------------
+def decode_attention_packed(q: torch.Tensor, packed_k: PackedTensor, packed_v: PackedTensor,
+                            num_attention_heads: int, block_n: int = 64) -> torch.Tensor:
+    """Packed-KV decode attention, K and V both per-token packed (``attention_triton.py:95-142``).
+
+    q ``[Hq, hd]`` fp16; packed_k/packed_v from ``quantize_pack(x, bits, -1, gs)`` over
+    ``[Hkv, S, hd]``.  Returns ``[Hq, hd]`` fp16.
+    """
+    hkv, s_len, hd = packed_k.orig_shape
+    if q.shape != (num_attention_heads, hd):
+        raise ValueError(f"q must be [Hq={num_attention_heads}, hd={hd}], got {tuple(q.shape)}")
+    if num_attention_heads % hkv != 0:
+        raise ValueError(f"Hq {num_attention_heads} is not a multiple of Hkv {hkv}")
+    vpb = _vals_per_byte(packed_k.bits)
+    gs = packed_k.group_size
+    if hd % vpb != 0 or hd % gs != 0:
+        raise ValueError(f"head_dim ({hd}) must be divisible by vpb ({vpb}) and group_size ({gs})")
+    seg = _dec.packed_segment(packed_k, packed_v, batched=False)
+    return _dec.fused_decode(_dec.Problem(q, [seg], num_attention_heads))[0]
+
+
+def _packed_split_launch(q: torch.Tensor, packed_k: PackedTensor, packed_v: PackedTensor,
+                         num_attention_heads: int, num_splits: int, block_n: int):
+    """Split-K partials (pm, pl, pacc) ``[Hq, num_splits(, hd)]`` (``attention_triton.py:216-254``).
+
+    ``num_splits = max(1, min(num_splits, S))`` splits of ``ceil(S / num_splits)``
+    tokens; trailing splits may be empty (m = -inf, l = 0, acc = 0).
+    """
+    hkv, s_len, hd = packed_k.orig_shape
+    if q.shape != (num_attention_heads, hd):
+        raise ValueError(f"q must be [Hq={num_attention_heads}, hd={hd}], got {tuple(q.shape)}")
+    num_splits = max(1, min(int(num_splits), s_len))
+    split_len = -(-s_len // num_splits)
+    seg = _dec.packed_segment(packed_k, packed_v, batched=False, splits=num_splits,
+                              split_len=split_len)
+    return _dec.decode_partials(_dec.Problem(q, [seg], num_attention_heads))
+
+
+def _reduce_splits(pm, pl, pacc):
+    """Merge split partials into one unnormalized (m, l, acc) (``attention_triton.py:257-266``)."""
+    return _dec.merge_partials(pm, pl, pacc, normalize=False)
+
+
+def decode_attention_packed_splitk(q: torch.Tensor, packed_k: PackedTensor,
+                                   packed_v: PackedTensor, num_attention_heads: int,
+                                   num_splits: int = 8, block_n: int = 64) -> torch.Tensor:
+    """Split-K packed decode (``attention_triton.py:269-276``), partials merged in the same launch."""
+    hkv, s_len, hd = packed_k.orig_shape
+    if q.shape != (num_attention_heads, hd):
+        raise ValueError(f"q must be [Hq={num_attention_heads}, hd={hd}], got {tuple(q.shape)}")
+    num_splits = max(1, min(int(num_splits), s_len))
+    split_len = -(-s_len // num_splits)
+    seg = _dec.packed_segment(packed_k, packed_v, batched=False, splits=num_splits,
+                              split_len=split_len)
+    return _dec.fused_decode(_dec.Problem(q, [seg], num_attention_heads))[0]
+
+
+def _packed_layer_partial(q, packed_k, packed_v, num_attention_heads, num_splits, block_n):
+    """(m, l, acc) of one per-token packed tier (``attention_triton.py:279-282``)."""
+    pm, pl, pacc = _packed_split_launch(q, packed_k, packed_v, num_attention_heads, num_splits,
+                                        block_n)
+    return _reduce_splits(pm, pl, pacc)
+
+
+def _fp16_layer_partial(q, hot_k, hot_v, num_attention_heads):
+    """(m, l, acc) of the FP16 hot tier ``[Hkv, hot, hd]`` (``attention_triton.py:285-297``).
+
+    The hot views are read in place through their strides (no GQA-expanded copies).
+    """
+    seg = _dec.fp16_segment(hot_k, hot_v, batched=False)
+    return _dec.decode_mlacc(_dec.Problem(q, [seg], num_attention_heads))
+
+
+def _merge_partials(partials):
+    """Cross-segment merge of (m, l, acc) partials -> ``[Hq, hd]`` fp16 (``attention_triton.py:300-307``)."""
+    if not partials:
+        raise ValueError("no partials to merge")
+    ms = torch.stack([p[0] for p in partials], dim=1)
+    ls = torch.stack([p[1] for p in partials], dim=1)
+    accs = torch.stack([p[2] for p in partials], dim=1)
+    return _dec.merge_partials(ms, ls, accs, normalize=True)
+
+
+# ---------------------------------------------------------------------------
+# three tiers in the legacy layout (attention_triton.py:310-511)
+# ---------------------------------------------------------------------------
+def _three_tier_segments(kv, num_splits):
+    segs = []
+    if kv.prompt_k is not None:
+        s_len = kv.prompt_k.orig_shape[1]
+        n = max(1, min(int(num_splits), s_len)) if num_splits else 0
+        segs.append(_dec.packed_segment(kv.prompt_k, kv.prompt_v, batched=False, splits=n,
+                                        split_len=(-(-s_len // n)) if n else 0))
+    if kv.cold_k is not None:
+        s_len = kv.cold_k.orig_shape[1]
+        n = max(1, min(int(num_splits), s_len)) if num_splits else 0
+        segs.append(_dec.packed_segment(kv.cold_k, kv.cold_v, batched=False, splits=n,
+                                        split_len=(-(-s_len // n)) if n else 0))
+    if kv.hot_k is not None and kv.hot_k.shape[1] > 0:
+        segs.append(_dec.fp16_segment(kv.hot_k.to(torch.float16), kv.hot_v.to(torch.float16),
+                                      batched=False))
+    if not segs:
+        raise ValueError("all three tiers are empty: nothing to attend")
+    return segs
+
+
+def fused_three_tier_decode(q, kv, num_attention_heads, num_splits: int = 8, block_n: int = 64):
+    """Prompt + cold (per-token packed) + FP16 hot attention (``attention_triton.py:487-511``).
+
+    q ``[Hq, hd]`` fp16; kv is a ``reference.ThreeTierKV`` with ``[Hkv, len, hd]`` tiers.
+    One launch; each packed tier is cut into ``num_splits`` splits as in the reference.
+    """
+    segs = _three_tier_segments(kv, num_splits)
+    return _dec.fused_decode(_dec.Problem(q, segs, num_attention_heads))[0]
+
+
+def fused_three_tier_decode_single(q, kv, num_attention_heads, num_splits: int = 32,
+                                   block_n: int = 64):
+    """Single-launch three-tier decode (``attention_triton.py:414-484``).
+
+    The reference's single launch predicates every tier's loads per token; here
+    each workgroup owns one tier's chunk, so the launch carries no cross-tier
+    redundancy.  Splits are chosen by the MI355X planner.
+    """
+    segs = _three_tier_segments(kv, 0)
+    return _dec.fused_decode(_dec.Problem(q, segs, num_attention_heads))[0]
+
+
+# ---------------------------------------------------------------------------
+# production KIVI path (attention_triton.py:514-669)
+# ---------------------------------------------------------------------------
+def _kivi_layer_partial(q, key: PackedTensor, value: PackedTensor, num_attention_heads: int,
+                        num_splits: int | None = None, block_n: int | None = None,
+                        num_warps: int | None = None):
+    """(m, l, acc) of one batch-stripped KIVI segment (``attention_triton.py:604-639``)."""
+    if key.axis != 1 or value.axis != 2 or len(key.orig_shape) != 3:
+        raise ValueError("K must be packed along tokens and V along head_dim, batch removed")
+    hkv, seq_len, head_dim = key.orig_shape
+    if tuple(value.orig_shape) != tuple(key.orig_shape) or seq_len <= 0:
+        raise ValueError("packed K/V shapes differ or the segment is empty")
+    if q.shape != (num_attention_heads, head_dim) or q.dtype != torch.float16:
+        raise ValueError("query must be [Hq, head_dim] float16")
+    if num_attention_heads % hkv or head_dim & (head_dim - 1):
+        raise ValueError("Hq must be a multiple of Hkv and head_dim a power of two")
+    if q.device != key.packed.device or q.device != value.packed.device:
+        raise ValueError("query and packed K/V must be on the same device")
+    splits, split_len = _override_plan(seq_len, num_attention_heads, head_dim, q.device,
+                                       num_splits, block_n, num_warps)
+    seg = _dec.packed_segment(key, value, batched=False, splits=splits, split_len=split_len)
+    return _dec.decode_mlacc(_dec.Problem(q, [seg], num_attention_heads))
+
+
+def _remove_batch(pt: PackedTensor) -> PackedTensor:
+    if pt.orig_shape[0] != 1:
+        raise ValueError("the PhaseKV decode path takes batch = 1 (use fused_phasekv_decode_batched)")
+    return replace(pt, packed=pt.packed[0], scale=pt.scale[0], mins=pt.mins[0],
+                   orig_shape=tuple(pt.orig_shape[1:]), axis=pt.axis - 1)
+
+
+def fused_phasekv_decode(q: torch.Tensor, tiers, num_attention_heads: int,
+                         num_splits: int | None = None, block_n: int | None = None,
+                         num_warps: int | None = None) -> torch.Tensor:
+    """batch=1 PhaseKV decode attention over every packed segment and the hot window.
+
+    ``tiers`` is ``PhaseKVCache.layer_tiers(i)`` (or any object with ``prompt``,
+    ``prompt_extensions``, ``cold``, ``hot_len`` and ``hot_views()``).  q ``[Hq, hd]``
+    fp16 -> ``[Hq, hd]`` fp16 (``attention_triton.py:643-669``).
+    """
+    segs = []
+    for segment in [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]:
+        key, value = _remove_batch(segment.key), _remove_batch(segment.value)
+        if key.axis != 1 or value.axis != 2:
+            raise ValueError("K must be packed along tokens and V along head_dim")
+        hkv, seq_len, head_dim = key.orig_shape
+        splits, split_len = _override_plan(seq_len, num_attention_heads, head_dim, q.device,
+                                           num_splits, block_n, num_warps)
+        segs.append(_dec.packed_segment(key, value, batched=False, splits=splits,
+                                        split_len=split_len))
+    if tiers.hot_len:
+        hot_k, hot_v = tiers.hot_views()
+        segs.append(_dec.fp16_segment(hot_k[0], hot_v[0], batched=False))
+    return _dec.fused_decode(_dec.Problem(q, segs, num_attention_heads))[0]
+
+
+def fused_phasekv_decode_batched(q: torch.Tensor, tiers, num_attention_heads: int,
+                                 prompt_lens: torch.Tensor | None = None) -> torch.Tensor:
+    """Batched PhaseKV decode: q ``[B, Hq, hd]`` over tiers with batch B -> ``[B, Hq, hd]``.
+
+    ``prompt_lens`` (int32 ``[B]`` on the device) gives ragged valid prompt
+    lengths; rows are quantized on their own (each row's K groups start at its
+    token 0) and padded to the tier's length.  Beyond the reference, which
+    takes batch = 1 only.
+    """
+    segs = []
+    for i, segment in enumerate([tiers.prompt, *tiers.prompt_extensions, *tiers.cold]):
+        lens = prompt_lens.to(torch.int32) if (i == 0 and prompt_lens is not None) else None
+        segs.append(_dec.packed_segment(segment.key, segment.value, batched=True, seq_lens=lens))
+    if tiers.hot_len:
+        hot_k, hot_v = tiers.hot_views()
+        segs.append(_dec.fp16_segment(hot_k, hot_v, batched=True))
+    return _dec.fused_decode(_dec.Problem(q, segs, num_attention_heads))
+
+
+def dense_fp16_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      num_attention_heads: int) -> torch.Tensor:
+    """GQA-aware FP16 decode attention over uncompressed K/V (the dense comparator).
+
+    q ``[Hq, hd]`` or ``[B, Hq, hd]``; k, v ``[Hkv, S, hd]`` or ``[B, Hkv, S, hd]`` fp16.
+    """
+    batched = q.dim() == 3
+    seg = _dec.fp16_segment(k, v, batched=batched)
+    out = _dec.fused_decode(_dec.Problem(q, [seg], num_attention_heads))
+    return out if batched else out[0]

@@ -1,0 +1,80 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol, and the
+ctypes mirrors of the structs match the C layout.  No compute calls (no GPU here)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from phasekv_amd import _lib
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HEADER = os.path.join(ROOT, "include", "phasekv_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pk_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert len(declared) >= 13
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.exported_symbols())
+
+
+def test_version_and_error_string_do_not_need_a_gpu():
+    lib = _lib.load()
+    assert b"gfx950" in lib.pk_version()
+    assert isinstance(lib.pk_last_error(), bytes)
+
+
+def test_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(r'''
+#include <stddef.h>
+#include <stdio.h>
+#include "phasekv_hip.h"
+#define F(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
+int main(void) {
+  printf("pk_segment %zu\n", sizeof(pk_segment));
+  printf("pk_decode_problem %zu\n", sizeof(pk_decode_problem));
+  F(pk_segment, seq_lens) F(pk_segment, k_data) F(pk_segment, v_mins)
+  F(pk_segment, k_data_bstride) F(pk_segment, tok_stride)
+  F(pk_decode_problem, q) F(pk_decode_problem, segments) F(pk_decode_problem, num_segments)
+  return 0;
+}
+''')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    out = dict(line.rsplit(" ", 1) for line in
+               subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+               if line)
+    assert int(out["pk_segment"]) == ctypes.sizeof(_lib.PkSegment)
+    assert int(out["pk_decode_problem"]) == ctypes.sizeof(_lib.PkDecodeProblem)
+    for key, val in out.items():
+        if "." in key:
+            struct, field = key.split(".")
+            cls = _lib.PkSegment if struct == "pk_segment" else _lib.PkDecodeProblem
+            assert getattr(cls, field).offset == int(val), key
+
+
+def test_python_side_rejects_bad_arguments_before_any_launch():
+    from phasekv_amd.kernels import packing
+    x = torch.zeros(1, 2, 8, 8, dtype=torch.float16)
+    with pytest.raises(ValueError, match="bits"):
+        packing.quantize_pack(x, 3, -1, 4)
+    with pytest.raises(ValueError, match="uint8"):
+        packing.pack_low_bits(torch.zeros(3, dtype=torch.int32), 2)
+    with pytest.raises(ValueError):
+        packing._vals_per_byte(5)
+    # no CPU path: a host tensor is refused, not computed with torch
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        packing.quantize_pack(x, 2, -1, 4)
