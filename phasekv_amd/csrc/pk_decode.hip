@@ -304,6 +304,10 @@ __global__ void zero_words_kernel(unsigned* p, int64_t n) {
 // ---------------------------------------------------------------------------
 // host-side planning
 // ---------------------------------------------------------------------------
+// Query heads per workgroup: q and acc of the slab stay within 2048 floats of
+// LDS each and at most 32 heads, so the generic kernel's LDS stays below 64 KB.
+static int head_slab(int G, int hd) { return std::min(G, std::min(32, std::max(1, 2048 / hd))); }
+
 static int validate_problem(const pk_decode_problem* p) {
   if (!p) return fail("null problem");
   if (p->batch <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0 || p->head_dim <= 0)
@@ -317,7 +321,7 @@ static int validate_problem(const pk_decode_problem* p) {
   if (p->num_segments <= 0 || !p->segments) return fail("no segments to attend");
   {
     const int G = p->num_q_heads / p->num_kv_heads;
-    const int HS = std::min(G, std::max(1, 2048 / hd));
+    const int HS = head_slab(G, hd);
     const int64_t counters = (int64_t)p->batch * p->num_kv_heads * cdiv(G, HS);
     if (counters * (int64_t)sizeof(unsigned) > PK_WORKSPACE_COUNTER_BYTES)
       return fail("batch * kv heads too large for the workspace counter region");
@@ -358,7 +362,7 @@ static Plan make_plan(const pk_decode_problem* p) {
   Plan pl{};
   const int hd = p->head_dim;
   pl.G = p->num_q_heads / p->num_kv_heads;
-  pl.HS = std::min(pl.G, std::max(1, 2048 / hd));
+  pl.HS = head_slab(pl.G, hd);
   pl.nslab = static_cast<int>(cdiv(pl.G, pl.HS));
   pl.tile = std::min(64, std::max(8, 4096 / hd));
   int64_t total_len = 0;

@@ -1,0 +1,118 @@
+"""HIP pack / unpack / quantize / dequantize vs the oracle: bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import packing_oracle as po
+from tests import golden_data
+
+pytestmark = pytest.mark.gpu
+
+
+def _to_torch(x_np, case, device):
+    if case["dtype"] == "bfloat16":
+        return torch.from_numpy(x_np.astype(np.int16)).view(torch.bfloat16).to(device)
+    return torch.from_numpy(x_np).to(device)
+
+
+def _u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy()
+
+
+def test_golden_vectors_through_hip(gpu):
+    from phasekv_amd.kernels import packing
+    z, man = golden_data.load()
+    for case in man["quantize"]:
+        x = _to_torch(z[case["input"]], case, gpu)
+        pt = packing.quantize_pack(x, case["bits"], case["axis"], case["group_size"])
+        k = case["key"]
+        assert pt.axis == case["out_axis"] and pt.group_size == case["out_group_size"], case
+        assert np.array_equal(pt.packed.cpu().numpy(), z[k + "_packed"]), case
+        assert np.array_equal(_u16(pt.scale), z[k + "_scale"].view(np.int16)), case
+        assert np.array_equal(_u16(pt.mins), z[k + "_mins"].view(np.int16)), case
+        deq = packing.unpack_dequantize(pt)
+        assert np.array_equal(_u16(deq), z[k + "_deq"].view(np.int16)), case
+    for case in man["pack"]:
+        k = case["key"]
+        codes = torch.from_numpy(z[k + "_codes"]).to(gpu)
+        packed = packing.pack_low_bits(codes, case["bits"])
+        assert np.array_equal(packed.cpu().numpy(), z[k + "_packed"])
+        un = packing.unpack_low_bits(packed, case["bits"], case["length"])
+        assert np.array_equal(un.cpu().numpy(), z[k + "_unpacked"])
+
+
+@pytest.mark.parametrize("shape,axis,gs", [
+    ((2, 3, 97, 16), -2, 32), ((2, 3, 97, 16), -1, 32), ((1, 4, 64, 128), -2, 32),
+    ((1, 4, 64, 128), -1, 32), ((3, 5, 7), 0, 2), ((1, 2, 33, 8), -2, 5), ((1, 2, 8, 33), -1, 7),
+    ((4, 1, 1, 8), -2, 1), ((1, 1, 300), -1, 1000),
+])
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_random_shapes_bit_exact(gpu, shape, axis, gs, bits):
+    from phasekv_amd.kernels import packing
+    g = torch.Generator().manual_seed(hash((shape, axis, gs, bits)) % 10000)
+    x = (torch.randn(*shape, generator=g) * 3).to(torch.float16)
+    pt = packing.quantize_pack(x.to(gpu), bits, axis, gs)
+    ref = po.quantize_pack(x.numpy(), bits, axis, gs)
+    assert pt.group_size == ref.group_size and pt.axis == ref.axis
+    assert np.array_equal(pt.packed.cpu().numpy(), ref.packed)
+    assert np.array_equal(_u16(pt.scale), ref.scale.view(np.int16))
+    assert np.array_equal(_u16(pt.mins), ref.mins.view(np.int16))
+    assert np.array_equal(_u16(packing.unpack_dequantize(pt)),
+                          po.unpack_dequantize(ref).view(np.int16))
+
+
+def test_strided_input_is_read_in_place(gpu):
+    from phasekv_amd.kernels import packing
+    g = torch.Generator().manual_seed(7)
+    base = torch.randn(2, 64, 3, 40, generator=g).to(torch.float16)
+    x = base.permute(0, 2, 1, 3)[:, :, 5:50]          # [2, 3, 45, 40] non-contiguous
+    xd = base.to(gpu).permute(0, 2, 1, 3)[:, :, 5:50]
+    assert not xd.is_contiguous()
+    for axis in (-1, -2):
+        pt = packing.quantize_pack(xd, 4, axis, 32)
+        ref = po.quantize_pack(x.contiguous().numpy(), 4, axis, 32)
+        assert np.array_equal(pt.packed.cpu().numpy(), ref.packed)
+        assert np.array_equal(_u16(pt.scale), ref.scale.view(np.int16))
+
+
+def test_bf16_and_fp32_inputs(gpu):
+    from phasekv_amd.kernels import packing
+    g = torch.Generator().manual_seed(9)
+    x32 = torch.randn(1, 2, 70, 16, generator=g)
+    for x in (x32, x32.to(torch.bfloat16)):
+        pt = packing.quantize_pack(x.to(gpu), 2, -2, 32)
+        ref = po.quantize_pack(x.float().numpy(), 2, -2, 32)
+        assert np.array_equal(pt.packed.cpu().numpy(), ref.packed)
+        assert np.array_equal(_u16(pt.scale), ref.scale.view(np.int16))
+
+
+def test_prefill_pack_block_full_size(gpu):
+    """C4 prefill: an 8192 x 4 x 128 fp16 K/V block packed to 2 bits, bit-exact."""
+    from phasekv_amd.kernels import packing
+    g = torch.Generator().manual_seed(1234)
+    k = torch.randn(1, 4, 8192, 128, generator=g).to(torch.float16)
+    v = torch.randn(1, 4, 8192, 128, generator=g).to(torch.float16)
+    kd, vd = k.to(gpu), v.to(gpu)
+    pk = packing.quantize_pack(kd, 2, -2, 32)
+    pv = packing.quantize_pack(vd, 2, -1, 32)
+    rk = po.quantize_pack(k.numpy(), 2, -2, 32)
+    rv = po.quantize_pack(v.numpy(), 2, -1, 32)
+    assert tuple(pk.packed.shape) == (1, 4, 128, 2048) and tuple(pv.packed.shape) == (1, 4, 8192, 32)
+    for pt, ref in ((pk, rk), (pv, rv)):
+        assert np.array_equal(pt.packed.cpu().numpy(), ref.packed)
+        assert np.array_equal(_u16(pt.scale), ref.scale.view(np.int16))
+        assert np.array_equal(_u16(pt.mins), ref.mins.view(np.int16))
+    # size-independent property: unpack(pack(codes)) == codes
+    codes = packing.unpack_low_bits(pk.packed, 2, 8192)
+    assert torch.equal(packing.pack_low_bits(codes, 2), pk.packed)
+
+
+def test_errors_are_value_errors(gpu):
+    from phasekv_amd.kernels import packing
+    x = torch.zeros(1, 2, 8, 8, dtype=torch.float16, device=gpu)
+    with pytest.raises(ValueError):
+        packing.quantize_pack(x, 3, -1, 4)
+    with pytest.raises(ValueError):
+        packing.quantize_pack(x[:, :, :0], 2, -2, 4)
+    with pytest.raises(ValueError):
+        packing.unpack_low_bits(torch.zeros(4, dtype=torch.int32, device=gpu), 2, 4)
