@@ -44,7 +44,6 @@ extern "C" {
 #define PK_SEG_FP16 2    /* uncompressed fp16 K/V [.., Hkv, S, hd], token stride given, hd contiguous */
 
 #define PK_MAX_SEGMENTS_PER_LAUNCH 8
-#define PK_WORKSPACE_COUNTER_BYTES 65536   /* counters of pk_fused_decode, at offset 0 */
 
 /* Last error message of the calling thread ("" if none). */
 const char* pk_last_error(void);
@@ -121,12 +120,14 @@ typedef struct pk_decode_problem {
   int64_t q_bstride, q_hstride;
   const pk_segment* segments;  /* host array */
   int32_t num_segments;
-  int32_t reserved;
+  int32_t flags;               /* PK_FLAG_* */
 } pk_decode_problem;
 
-/* Bytes of split-K workspace pk_decode_partials needs for this problem
- * (a fixed PK_WORKSPACE_COUNTER_BYTES counter region first, then the partials
- * m, l [batch*Hq][splits] and acc [batch*Hq][splits][hd] fp32).  Replaces the torch.empty
+#define PK_FLAG_GENERIC_KERNEL 1   /* use the general-shape kernel even where the MFMA one applies */
+
+/* Bytes of split-K workspace pk_decode_partials needs for this problem: the
+ * partials m, l [batch*Hq][splits] and acc [batch*Hq][splits][hd] fp32, each
+ * region 256-byte aligned, in that order.  Replaces the torch.empty
  * partial buffers of _kivi_layer_partial (attention_triton.py:624-626). */
 int pk_decode_workspace_size(const pk_decode_problem* p, size_t* bytes, int32_t* total_splits);
 
@@ -146,19 +147,14 @@ int pk_decode_partials(const pk_decode_problem* p, void* workspace, size_t works
 int pk_decode_combine(const pk_decode_problem* p, const void* workspace, uint16_t* out,
                       float* out_m, float* out_l, float* out_acc, void* stream);
 
-/* Partials + combine in one launch: the last workgroup of each (batch, kv head)
- * merges the splits (no second launch).  The counter region at the start of
- * the workspace must be zero when the call starts; every call leaves it at
- * zero, so a freshly allocated workspace is zeroed once with
- * pk_decode_workspace_init and can then be reused by any problem.  Calls that
- * share a workspace must be ordered (same stream).  Same result as
- * pk_decode_partials followed by pk_decode_combine(out). */
+/* pk_decode_partials followed by pk_decode_combine(out) on the same stream: the
+ * whole decode step of every segment in two launches (one partial launch per
+ * PK_MAX_SEGMENTS_PER_LAUNCH segments).  Replaces fused_phasekv_decode's
+ * per-segment launches, _reduce_splits and _merge_partials
+ * (attention_triton.py:643-669).  Calls sharing a workspace must be ordered
+ * (same stream). */
 int pk_fused_decode(const pk_decode_problem* p, void* workspace, size_t workspace_bytes,
                     uint16_t* out, void* stream);
-
-/* Zero the counter region of a decode workspace (a fill kernel, not a memset).
- * workspace_bytes must be >= PK_WORKSPACE_COUNTER_BYTES. */
-int pk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Merge n partials per row: m, l [rows, n] and acc [rows, n, hd] fp32 contiguous.
  * Writes normalized fp16 out [rows, hd] (_merge_partials, attention_triton.py:300-307)

@@ -27,7 +27,7 @@ PK_SEG_TOKEN = 1
 PK_SEG_FP16 = 2
 
 PK_MAX_SEGMENTS_PER_LAUNCH = 8
-PK_WORKSPACE_COUNTER_BYTES = 65536
+PK_FLAG_GENERIC_KERNEL = 1
 
 _c_i32 = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -59,7 +59,7 @@ class PkDecodeProblem(ctypes.Structure):
         ("head_dim", _c_i32),
         ("q", _c_vp), ("q_bstride", _c_i64), ("q_hstride", _c_i64),
         ("segments", ctypes.POINTER(PkSegment)), ("num_segments", _c_i32),
-        ("reserved", _c_i32),
+        ("flags", _c_i32),
     ]
 
 
@@ -89,7 +89,6 @@ _SIGNATURES = {
                                          _c_vp, _c_vp, _c_vp]),
     "pk_fused_decode": (ctypes.c_int, [ctypes.POINTER(PkDecodeProblem), _c_vp, ctypes.c_size_t,
                                        _c_vp, _c_vp]),
-    "pk_decode_workspace_init": (ctypes.c_int, [_c_vp, ctypes.c_size_t, _c_vp]),
     "pk_merge_partials": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32, _c_vp,
                                          _c_vp, _c_vp, _c_vp, _c_vp]),
 }

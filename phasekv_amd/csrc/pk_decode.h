@@ -8,7 +8,7 @@ namespace pk {
 constexpr int kThreads = 256;                 // threads per decode workgroup
 constexpr int kMaxSeg = PK_MAX_SEGMENTS_PER_LAUNCH;
 constexpr int kCombineMaxHd = 256;            // largest head_dim handled by the combine
-constexpr int kCombineChunk = 1024;           // partial weights staged in LDS per pass
+constexpr int kCombineRegs = 32;             // partial loads in flight per combine thread
 constexpr int kMinChunk = 64;                 // auto chunk lengths are multiples of this
 
 // One segment as the kernels see it (element strides, see pk_segment).
@@ -36,14 +36,14 @@ struct DecodeParams {
   float* ws_m;        // [B*Hq][C]
   float* ws_l;        // [B*Hq][C]
   float* ws_acc;      // [B*Hq][C][hd]
-  unsigned* counters; // [B*Hkv*nslab], zero between calls
   int C;              // chunks per (batch, kv head) over all segments
   int nseg;
-  int fused;          // last workgroup of a (batch, kv head, slab) writes the output
-  uint16_t* out;      // [B*Hq][hd] fp16 when fused
+  int wave_lds;       // MFMA kernel: LDS bytes of one wave's tile staging
   SegDev seg[kMaxSeg];
 };
 
-__global__ void zero_words_kernel(unsigned* p, int64_t n);
+// MFMA fast path (pk_decode_mfma.hip): same parameters and partial layout.
+int launch_decode_mfma(const DecodeParams& dp, int lchunks, int max_kbits, int max_vbits,
+                       hipStream_t stream);
 
 }  // namespace pk

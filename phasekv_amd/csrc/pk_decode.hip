@@ -18,6 +18,8 @@
 
 #include <math.h>
 
+#include <stdlib.h>
+
 #include <algorithm>
 #include <vector>
 
@@ -50,78 +52,6 @@ __device__ __forceinline__ float token_elem(const uint8_t* data, const uint16_t*
   return static_cast<float>(code) * pk_h2f(sc[m_off + g]) + pk_h2f(mn[m_off + g]);
 }
 
-// Whole-workgroup log-sum-exp merge of one output row's C partials.
-__device__ void combine_row(const float* __restrict__ m, const float* __restrict__ l,
-                            const float* __restrict__ acc, int C, int hd, int64_t row,
-                            uint16_t* out, float* om, float* ol, float* oacc, float* w_s,
-                            int w_cap, float* red_s) {
-  const int tid = threadIdx.x;
-  const int nt = blockDim.x;
-  const float* mr = m + row * C;
-  const float* lr = l + row * C;
-  const float* ar = acc + row * C * (int64_t)hd;
-  float mx = -INFINITY;
-  for (int c = tid; c < C; c += nt) mx = fmaxf(mx, mr[c]);
-  red_s[tid] = mx;
-  __syncthreads();
-  for (int s = nt / 2; s > 0; s >>= 1) {
-    if (tid < s) red_s[tid] = fmaxf(red_s[tid], red_s[tid + s]);
-    __syncthreads();
-  }
-  const float M = red_s[0];
-  __syncthreads();
-  float lsum = 0.f;
-  // accumulators for up to kCombineMaxHd / nt channels per thread
-  float a[kCombineMaxHd / kThreads];
-#pragma unroll
-  for (int i = 0; i < kCombineMaxHd / kThreads; ++i) a[i] = 0.f;
-  const int chunk = min(kCombineChunk, w_cap);
-  for (int c0 = 0; c0 < C; c0 += chunk) {
-    const int cn = min(chunk, C - c0);
-    for (int c = tid; c < cn; c += nt) {
-      const float mc = mr[c0 + c];
-      const float w = (mc == -INFINITY) ? 0.f : expf(mc - M);
-      w_s[c] = w;
-      lsum += w * lr[c0 + c];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kCombineMaxHd / kThreads; ++i) {
-      const int d = tid + i * nt;
-      if (d < hd) {
-        float s = a[i];
-        for (int c = 0; c < cn; ++c) s += w_s[c] * ar[(int64_t)(c0 + c) * hd + d];
-        a[i] = s;
-      }
-    }
-    __syncthreads();
-  }
-  red_s[tid] = lsum;
-  __syncthreads();
-  for (int s = nt / 2; s > 0; s >>= 1) {
-    if (tid < s) red_s[tid] += red_s[tid + s];
-    __syncthreads();
-  }
-  const float L = red_s[0];
-  __syncthreads();
-  if (out) {
-    const float inv = 1.0f / L;
-#pragma unroll
-    for (int i = 0; i < kCombineMaxHd / kThreads; ++i) {
-      const int d = tid + i * nt;
-      if (d < hd) out[row * hd + d] = pk_f2h(a[i] * inv);
-    }
-  }
-  if (om && tid == 0) { om[row] = M; ol[row] = L; }
-  if (oacc) {
-#pragma unroll
-    for (int i = 0; i < kCombineMaxHd / kThreads; ++i) {
-      const int d = tid + i * nt;
-      if (d < hd) oacc[row * hd + d] = a[i];
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // generic partial kernel (any power-of-two hd <= 256, any bits / group sizes)
 // ---------------------------------------------------------------------------
@@ -140,7 +70,6 @@ decode_partials_generic(const DecodeParams p) {
   float* m_s = p_s + HS * T;              // [HS]
   float* l_s = m_s + HS;                  // [HS]
   float* a_s = l_s + HS;                  // [HS]
-  __shared__ int sh_last;
 
   const int b = blockIdx.z;
   const int kvh = blockIdx.y / p.nslab;
@@ -261,44 +190,91 @@ decode_partials_generic(const DecodeParams p) {
     p.ws_m[row * p.C + cg] = m_s[h];
     p.ws_l[row * p.C + cg] = l_s[h];
   }
-  if (!p.fused) return;
-
-  // ---- fused combine: the last workgroup of this (b, kv head, slab) merges ----
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    unsigned* ctr = p.counters + ((int64_t)b * p.Hkv + kvh) * p.nslab + slab;
-    const unsigned prev = atomicAdd(ctr, 1u);
-    const int last = (prev == (unsigned)(p.C - 1));
-    if (last) atomicExch(ctr, 0u);   // leave the counter at zero for the next call
-    sh_last = last;
-  }
-  __syncthreads();
-  if (!sh_last) return;
-  __threadfence();
-  // LDS reuse: the tile buffers are free now.
-  float* w_s = k_s;
-  float* red_s = v_s;
-  for (int h = 0; h < nh; ++h) {
-    const int64_t row = (int64_t)b * p.Hq + h0 + h;
-    combine_row(p.ws_m, p.ws_l, p.ws_acc, p.C, hd, row, p.out, nullptr, nullptr, nullptr, w_s,
-                T * (hd + 1), red_s);
-  }
 }
 
+// Log-sum-exp merge of the C partials of one output row per workgroup
+// (attention_triton.py:257-266, 300-307).  Thread (cs, d) owns channel d of
+// partials cs, cs + ncs, ...: it issues all of its loads (up to kCombineRegs
+// per pass) before using any, together with the row's m / l, so a pass costs
+// one memory round trip; the weights exp(m_c - M) go through LDS and the
+// channel sums of the ncs slices are added through LDS.
 __global__ void __launch_bounds__(kThreads)
 combine_kernel(const float* __restrict__ m, const float* __restrict__ l,
                const float* __restrict__ acc, int C, int hd, uint16_t* out, float* om, float* ol,
                float* oacc) {
-  __shared__ float w_s[kCombineChunk];
-  __shared__ float red_s[kThreads];
-  combine_row(m, l, acc, C, hd, blockIdx.x, out, om, ol, oacc, w_s, kCombineChunk, red_s);
-}
-
-__global__ void zero_words_kernel(unsigned* p, int64_t n) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = 0u;
+  extern __shared__ float cw[];             // [C] weights
+  __shared__ float red[kThreads];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* mr = m + row * C;
+  const float* lr = l + row * C;
+  const float* ar = acc + row * (int64_t)C * hd;
+  const int ncs = kThreads / hd;            // hd <= 256, a power of two
+  const int d = tid % hd, cs = tid / hd;
+  float sum = 0.f, ls = 0.f;
+  float M = -INFINITY;
+  for (int base = 0; base < C; base += kCombineRegs * ncs) {
+    // ---- issue every load of this pass ----
+    float a[kCombineRegs];
+#pragma unroll
+    for (int k = 0; k < kCombineRegs; ++k) {
+      const int c = base + cs + k * ncs;
+      a[k] = (c < C) ? ar[(int64_t)c * hd + d] : 0.f;
+    }
+    float mloc = -INFINITY;
+    float lloc = 0.f;
+    for (int c = base + tid; c < min(C, base + kCombineRegs * ncs); c += kThreads) {
+      const float mc = mr[c];
+      cw[c - base] = mc;
+      mloc = fmaxf(mloc, mc);
+    }
+    // ---- running max over the passes so far ----
+    red[tid] = mloc;
+    __syncthreads();
+    for (int st = kThreads / 2; st > 0; st >>= 1) {
+      if (tid < st) red[tid] = fmaxf(red[tid], red[tid + st]);
+      __syncthreads();
+    }
+    const float Mn = fmaxf(M, red[0]);
+    const float scale_old = (M == -INFINITY) ? 0.f : expf(M - Mn);
+    M = Mn;
+    __syncthreads();
+    for (int c = base + tid; c < min(C, base + kCombineRegs * ncs); c += kThreads) {
+      const float mc = cw[c - base];
+      const float w = (mc == -INFINITY) ? 0.f : expf(mc - M);
+      cw[c - base] = w;
+      lloc += w * lr[c];
+    }
+    __syncthreads();
+    float part = 0.f;
+#pragma unroll
+    for (int k = 0; k < kCombineRegs; ++k) {
+      const int c = base + cs + k * ncs;
+      if (c < C) part += cw[c - base] * a[k];
+    }
+    sum = sum * scale_old + part;
+    ls = ls * scale_old + lloc;
+    __syncthreads();
+  }
+  red[tid] = ls;
+  __syncthreads();
+  for (int st = kThreads / 2; st > 0; st >>= 1) {
+    if (tid < st) red[tid] += red[tid + st];
+    __syncthreads();
+  }
+  const float L = red[0];
+  __syncthreads();
+  red[tid] = sum;
+  __syncthreads();
+  if (cs == 0) {
+    for (int k = 1; k < ncs; ++k) sum += red[k * hd + d];
+    if (out) out[row * hd + d] = pk_f2h(sum / L);
+    if (oacc) oacc[row * hd + d] = sum;
+  }
+  if (om && tid == 0) {
+    om[row] = M;
+    ol[row] = L;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -319,13 +295,6 @@ static int validate_problem(const pk_decode_problem* p) {
   if (hd > kCombineMaxHd) return fail("head_dim above 256 is not supported");
   if (!p->q) return fail("null q");
   if (p->num_segments <= 0 || !p->segments) return fail("no segments to attend");
-  {
-    const int G = p->num_q_heads / p->num_kv_heads;
-    const int HS = head_slab(G, hd);
-    const int64_t counters = (int64_t)p->batch * p->num_kv_heads * cdiv(G, HS);
-    if (counters * (int64_t)sizeof(unsigned) > PK_WORKSPACE_COUNTER_BYTES)
-      return fail("batch * kv heads too large for the workspace counter region");
-  }
   for (int i = 0; i < p->num_segments; ++i) {
     const pk_segment& s = p->segments[i];
     if (s.length <= 0) return fail("segment " + std::to_string(i) + " is empty");
@@ -352,26 +321,90 @@ static int validate_problem(const pk_decode_problem* p) {
 }
 
 struct Plan {
+  bool mfma;            // MFMA fast path (else the generic kernel)
   int G, HS, nslab, tile;
   int C;
+  int max_kbits, max_vbits;
   std::vector<int> n_chunks, chunk_len, gbegin;
   size_t off_m, off_l, off_acc, bytes;
 };
 
+static bool aligned(const void* ptr, int64_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
+
+// The MFMA kernel covers head_dim 64 / 128, FP16 segments with 16-byte aligned
+// rows and KIVI segments with 32-token K groups (or a single group) and 32-channel
+// V groups; explicit split lengths must be whole 32-token groups.
+static bool mfma_eligible(const pk_decode_problem* p) {
+  if (p->flags & PK_FLAG_GENERIC_KERNEL) return false;
+  const int hd = p->head_dim;
+  if (hd != 64 && hd != 128) return false;
+  if (!aligned(p->q, 16) || p->q_hstride % 8 || p->q_bstride % 8) return false;
+  for (int i = 0; i < p->num_segments; ++i) {
+    const pk_segment& s = p->segments[i];
+    if (s.splits > 0) {
+      const int64_t cl = s.split_len > 0 ? s.split_len
+                                         : cdiv(s.length, std::min<int64_t>(s.length, s.splits));
+      const int64_t nc = s.split_len > 0 ? s.splits : cdiv(s.length, cl);
+      if (nc > 1 && cl % 32) return false;
+    }
+    if (s.kind == PK_SEG_FP16) {
+      if (s.tok_stride % 8 || !aligned(s.k_data, 16) || !aligned(s.v_data, 16)) return false;
+      if (s.k_data_bstride % 8 || s.k_data_hstride % 8 || s.v_data_bstride % 8 ||
+          s.v_data_hstride % 8)
+        return false;
+      continue;
+    }
+    if (s.kind != PK_SEG_KIVI) return false;
+    if (!(s.k_group == 32 || s.k_group >= s.length) || s.v_group != 32) return false;
+    const int64_t row_bytes = ((int64_t)s.length * s.k_bits + 7) / 8;
+    const int64_t kcb = (s.k_bits == 2) ? 8 : 16;   // K load width of the kernel
+    const int64_t ra = (row_bytes % kcb == 0) ? kcb : (row_bytes % 4 == 0) ? 4 : 1;
+    if (!aligned(s.k_data, ra) || s.k_data_bstride % ra || s.k_data_hstride % ra) return false;
+    if (!aligned(s.v_data, 16) || s.v_data_bstride % 16 || s.v_data_hstride % 16) return false;
+  }
+  return true;
+}
+
+static int64_t env_int(const char* name, int64_t dflt) {
+  const char* v = getenv(name);
+  if (!v || !*v) return dflt;
+  return std::max<int64_t>(1, atoll(v));
+}
+
 static Plan make_plan(const pk_decode_problem* p) {
   Plan pl{};
   const int hd = p->head_dim;
+  pl.mfma = mfma_eligible(p);
   pl.G = p->num_q_heads / p->num_kv_heads;
-  pl.HS = head_slab(pl.G, hd);
+  pl.HS = pl.mfma ? std::min(pl.G, 16) : head_slab(pl.G, hd);
   pl.nslab = static_cast<int>(cdiv(pl.G, pl.HS));
   pl.tile = std::min(64, std::max(8, 4096 / hd));
   int64_t total_len = 0;
-  for (int i = 0; i < p->num_segments; ++i) total_len += p->segments[i].length;
+  pl.max_kbits = 2;
+  pl.max_vbits = 2;
+  for (int i = 0; i < p->num_segments; ++i) {
+    const pk_segment& s = p->segments[i];
+    total_len += s.length;
+    if (s.kind != PK_SEG_FP16) {
+      pl.max_kbits = std::max(pl.max_kbits, s.k_bits);
+      pl.max_vbits = std::max(pl.max_vbits, s.v_bits);
+    }
+  }
   const int64_t per_bh = (int64_t)p->batch * p->num_kv_heads * pl.nslab;
-  const int64_t want = 4LL * device_cu_count();
-  const int64_t chunks_target = std::max<int64_t>(1, cdiv(want, per_bh));
-  int64_t auto_len = cdiv(total_len, chunks_target);
-  auto_len = std::max<int64_t>(kMinChunk, cdiv(auto_len, kMinChunk) * kMinChunk);
+  int64_t auto_len;
+  if (pl.mfma) {
+    // about two 4-wave workgroups per CU, chunks of whole 128-token rounds (one
+    // 32-token group per wave), so few partials per row reach the combine
+    const int64_t want = env_int("PK_TARGET_WORKGROUPS", 2LL * device_cu_count());
+    auto_len = cdiv(cdiv(total_len * per_bh, want), 128) * 128;
+    auto_len = env_int("PK_CHUNK_TOKENS", std::max<int64_t>(128, auto_len));
+    auto_len = cdiv(auto_len, 32) * 32;
+  } else {
+    const int64_t want = 4LL * device_cu_count();
+    const int64_t chunks_target = std::max<int64_t>(1, cdiv(want, per_bh));
+    auto_len = cdiv(total_len, chunks_target);
+    auto_len = std::max<int64_t>(kMinChunk, cdiv(auto_len, kMinChunk) * kMinChunk);
+  }
   pl.C = 0;
   for (int i = 0; i < p->num_segments; ++i) {
     const pk_segment& s = p->segments[i];
@@ -394,7 +427,7 @@ static Plan make_plan(const pk_decode_problem* p) {
   }
   const int64_t rows = (int64_t)p->batch * p->num_q_heads;
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
-  pl.off_m = PK_WORKSPACE_COUNTER_BYTES;
+  pl.off_m = 0;
   pl.off_l = align(pl.off_m + rows * pl.C * sizeof(float));
   pl.off_acc = align(pl.off_l + rows * pl.C * sizeof(float));
   pl.bytes = align(pl.off_acc + rows * pl.C * (size_t)hd * sizeof(float));
@@ -427,8 +460,8 @@ static size_t generic_lds_bytes(const Plan& pl, int hd) {
                           (size_t)pl.HS * pl.tile + 3 * pl.HS);
 }
 
-static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws, bool fused,
-                           uint16_t* out, hipStream_t stream) {
+static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
+                           hipStream_t stream) {
   DecodeParams dp{};
   dp.B = p->batch;
   dp.Hq = p->num_q_heads;
@@ -445,10 +478,7 @@ static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
   dp.ws_m = reinterpret_cast<float*>(ws + pl.off_m);
   dp.ws_l = reinterpret_cast<float*>(ws + pl.off_l);
   dp.ws_acc = reinterpret_cast<float*>(ws + pl.off_acc);
-  dp.counters = reinterpret_cast<unsigned*>(ws);
   dp.C = pl.C;
-  dp.fused = fused ? 1 : 0;
-  dp.out = out;
   const size_t lds = generic_lds_bytes(pl, p->head_dim);
   for (int first = 0; first < p->num_segments; first += kMaxSeg) {
     const int n = std::min(kMaxSeg, p->num_segments - first);
@@ -463,9 +493,14 @@ static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
       lchunks += d.n_chunks;
     }
     dp.nseg = n;
-    dim3 grid(lchunks, p->num_kv_heads * pl.nslab, p->batch);
-    hipLaunchKernelGGL(decode_partials_generic, grid, dim3(kThreads), lds, stream, dp);
-    int rc = check_launch("decode_partials");
+    int rc;
+    if (pl.mfma) {
+      rc = launch_decode_mfma(dp, lchunks, pl.max_kbits, pl.max_vbits, stream);
+    } else {
+      dim3 grid(lchunks, p->num_kv_heads * pl.nslab, p->batch);
+      hipLaunchKernelGGL(decode_partials_generic, grid, dim3(kThreads), lds, stream, dp);
+      rc = check_launch("decode_partials");
+    }
     if (rc) return rc;
   }
   return PK_OK;
@@ -493,8 +528,17 @@ extern "C" int pk_decode_partials(const pk_decode_problem* p, void* workspace,
   if (rc) return rc;
   Plan pl = make_plan(p);
   if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
-  return launch_partials(p, pl, static_cast<char*>(workspace), false, nullptr,
-                         static_cast<hipStream_t>(stream));
+  return launch_partials(p, pl, static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+}
+
+static int launch_combine(const float* m, const float* l, const float* acc, int64_t rows, int C,
+                          int hd, uint16_t* out, float* om, float* ol, float* oacc,
+                          hipStream_t stream, const char* what) {
+  if (rows == 0) return PK_OK;
+  const size_t lds = sizeof(float) * (size_t)std::min(C, kCombineRegs * kThreads);
+  hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(kThreads), lds, stream, m, l, acc, C, hd,
+                     out, om, ol, oacc);
+  return check_launch(what);
 }
 
 extern "C" int pk_decode_combine(const pk_decode_problem* p, const void* workspace,
@@ -507,24 +551,11 @@ extern "C" int pk_decode_combine(const pk_decode_problem* p, const void* workspa
   if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
   Plan pl = make_plan(p);
   const char* ws = static_cast<const char*>(workspace);
-  const int64_t rows = (int64_t)p->batch * p->num_q_heads;
-  hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream),
-                     reinterpret_cast<const float*>(ws + pl.off_m),
-                     reinterpret_cast<const float*>(ws + pl.off_l),
-                     reinterpret_cast<const float*>(ws + pl.off_acc), pl.C, p->head_dim, out,
-                     out_m, out_l, out_acc);
-  return check_launch("decode_combine");
-}
-
-extern "C" int pk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  if (!workspace) return fail("null workspace");
-  if (workspace_bytes < PK_WORKSPACE_COUNTER_BYTES) return fail("workspace smaller than its counter region");
-  const int64_t words = PK_WORKSPACE_COUNTER_BYTES / 4;
-  hipLaunchKernelGGL(zero_words_kernel, dim3(cdiv(words, kThreads)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), static_cast<unsigned*>(workspace), words);
-  return check_launch("decode_workspace_init");
+  return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
+                        reinterpret_cast<const float*>(ws + pl.off_l),
+                        reinterpret_cast<const float*>(ws + pl.off_acc),
+                        (int64_t)p->batch * p->num_q_heads, pl.C, p->head_dim, out, out_m, out_l,
+                        out_acc, static_cast<hipStream_t>(stream), "decode_combine");
 }
 
 extern "C" int pk_fused_decode(const pk_decode_problem* p, void* workspace, size_t workspace_bytes,
@@ -536,12 +567,14 @@ extern "C" int pk_fused_decode(const pk_decode_problem* p, void* workspace, size
   Plan pl = make_plan(p);
   if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (p->num_segments <= kMaxSeg) {
-    return launch_partials(p, pl, static_cast<char*>(workspace), true, out, s);
-  }
-  rc = launch_partials(p, pl, static_cast<char*>(workspace), false, nullptr, s);
+  rc = launch_partials(p, pl, static_cast<char*>(workspace), s);
   if (rc) return rc;
-  return pk_decode_combine(p, workspace, out, nullptr, nullptr, nullptr, stream);
+  const char* ws = static_cast<const char*>(workspace);
+  return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
+                        reinterpret_cast<const float*>(ws + pl.off_l),
+                        reinterpret_cast<const float*>(ws + pl.off_acc),
+                        (int64_t)p->batch * p->num_q_heads, pl.C, p->head_dim, out, nullptr,
+                        nullptr, nullptr, s, "fused_decode");
 }
 
 extern "C" int pk_merge_partials(const float* m, const float* l, const float* acc, int64_t rows,
@@ -549,12 +582,10 @@ extern "C" int pk_merge_partials(const float* m, const float* l, const float* ac
                                  float* out_l, float* out_acc, void* stream) {
   clear_error();
   if (rows < 0 || n <= 0 || head_dim <= 0) return fail("rows, n and head_dim must be positive");
-  if (head_dim > kCombineMaxHd) return fail("head_dim above 256 is not supported");
+  if (head_dim > kCombineMaxHd || (head_dim & (head_dim - 1)))
+    return fail("head_dim must be a power of two <= 256");
   if (!m || !l || !acc) return fail("null partials");
   if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
-  if (rows == 0) return PK_OK;
-  hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), m, l, acc, n, head_dim, out, out_m, out_l,
-                     out_acc);
-  return check_launch("merge_partials");
+  return launch_combine(m, l, acc, rows, n, head_dim, out, out_m, out_l, out_acc,
+                        static_cast<hipStream_t>(stream), "merge_partials");
 }

@@ -1,0 +1,760 @@
+// MFMA decode attention over packed KIVI segments and FP16 segments (gfx950).
+//
+// Same work list, partial layout and combine as the generic kernel; this file
+// is the fast path for head_dim 64 / 128, KIVI segments with group size 32 (or
+// a single group) and FP16 segments.  Reference semantics: the per-segment
+// kernel src/phasekv/kernels/attention_triton.py:514-596 and the FP16 hot
+// partial attention_triton.py:285-297.
+//
+// One workgroup = 4 waves = one (chunk, batch row, kv head, head slab).  Each
+// wave takes 32-token groups (one K quantization group) of the chunk round
+// robin, keeps its own online softmax state and prefetches its next group
+// while computing the current one; the waves merge through LDS and the
+// workgroup writes one partial.
+//
+// Math per 32-token quantization group (K is packed per channel, V per token):
+//   scores  S^T[t][h] = sum_c code_K[t][c] * (q[h][c] * sK[c][g])  +  sum_c q[h][c] * mK[c][g]
+//   output  O^T[c][h] = sum_t code_V[t][c] * (p[t][h] * sV[t][cg]) +  sum_t p[t][h] * mV[t][cg]
+// so the per-channel K scale is folded into q and the per-token V scale into
+// p; the code matrices go straight into v_mfma_f32_16x16x32_f16.
+//
+// Codes reach the MFMA without any int->float conversion: a byte permute puts
+// two codes (two channels of one token for K, two tokens of one channel for
+// V) into the low bits of the two fp16 halves of a register and an AND keeps
+// them.  An fp16 with exponent field 0 is the subnormal  mantissa * 2^-24,
+// so the register holds  code * 2^(24 - position bits)  exactly; the matrix
+// cores take fp16 subnormals without flushing, and the power-of-two factors
+// are undone on the fp32 results (per score row, per output row).
+//
+// MFMA 16x16x32 f16 operand layout (lane l, slot j): A[l%16][8*(l/16)+j],
+// B[8*(l/16)+j][l%16]; result D[4*(l/16)+e][l%16] in register e.
+#include "pk_common.h"
+#include "pk_decode.h"
+
+#include <math.h>
+
+namespace pk {
+namespace {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;
+constexpr int kTile = 32;            // tokens per wave step (one K group)
+constexpr float kTwo24 = 16777216.0f;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr uint32_t kOnes2 = 0x3C003C00u;   // fp16 pair (1.0, 1.0)
+
+__device__ __forceinline__ f4_t mfma(u4_t a, u4_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
+                                                __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+
+// result byte k <- selector byte k: 0..3 pick bytes of `lo`, 4..7 bytes of `hi`, 0x0c gives 0
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// selector: byte b of lo -> byte 0, byte b of hi -> byte 2, zeros elsewhere
+__device__ __forceinline__ uint32_t sel_bytes(int b) {
+  return (uint32_t)b | (0x0cu << 8) | ((uint32_t)(4 + b) << 16) | (0x0cu << 24);
+}
+
+// selector: half hh of lo -> low half, half hh of hi -> high half
+__device__ __forceinline__ uint32_t sel_halves(int hh) {
+  const uint32_t b = 2u * hh;
+  return b | ((b + 1) << 8) | ((b + 4) << 16) | ((b + 5) << 24);
+}
+
+__device__ __forceinline__ uint32_t pkmul(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, a) * __builtin_bit_cast(h2_t, b));
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  h2_t v = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Sums / maxima over the four 16-lane rows of a wave that hold the same head
+// column: v_permlane16_swap and v_permlane32_swap exchange rows in the VALU,
+// with no trip through the LDS crossbar.
+__device__ __forceinline__ float xsum4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float v2 = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v2), __float_as_uint(v2), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ float xmax4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float v2 = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v2), __float_as_uint(v2), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ u4_t lds_u4(const char* p) { return *reinterpret_cast<const u4_t*>(p); }
+__device__ __forceinline__ u2_t lds_u2(const char* p) { return *reinterpret_cast<const u2_t*>(p); }
+__device__ __forceinline__ uint32_t lds_u32(const char* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// Running softmax state of one wave (lane = head column n, lane group g4).
+template <int HD>
+struct WaveAcc {
+  f4_t o[HD / 16];     // O^T blocks: rows 4*g4 + e of channel block b, column = head
+  float vb[HD / 32];   // sum_t p * mV  (this lane's tokens)
+  float m;             // running max, log2 units, same in the 4 lane groups
+  float l;             // sum_t p (this lane's tokens)
+};
+
+// ---------------------------------------------------------------------------
+// per-wave LDS staging of one 32-token KIVI group
+//   Kw  uint32 [KB][HD]         the group's K bytes of every channel row
+//   Ks, Km  fp16 [HD]           K scale / min of the group
+//   Vw  uint32 [32][HD*VB/32]   the group's V rows
+//   Vs, Vm  fp16 [HD/32][32]    V scale / min, channel group major
+// ---------------------------------------------------------------------------
+template <int HD, int KB, int VB>
+struct KiviLayout {
+  static constexpr int kw_bytes = KB * HD * 4;
+  static constexpr int vrow_words = HD * VB / 32;
+  static constexpr int vrow_bytes = HD * VB / 8;
+  static constexpr int vw_bytes = kTile * vrow_bytes;
+  static constexpr int off_ks = kw_bytes;
+  static constexpr int off_km = off_ks + 2 * HD;
+  static constexpr int off_vw = off_km + 2 * HD;
+  static constexpr int off_vs = off_vw + vw_bytes;
+  static constexpr int off_vm = off_vs + 2 * HD;
+  static constexpr int bytes = off_vm + 2 * HD;
+};
+
+// Registers of one group's global loads.  Every address is clamped into the
+// segment, so the loads are unconditional and a whole group's loads are
+// in flight together; K bytes of tokens past the end give scores that are
+// masked, and V rows / metadata of such tokens are multiplied by p = 0.
+template <int HD, int KB, int VB>
+struct GroupRegs {
+  static constexpr int KCB = (KB == 2) ? 8 : 16;          // bytes per K load
+  static constexpr int KCR = 4 * KB / KCB;                // K loads per channel row
+  static constexpr int NK = HD * KCR / 64;                // K loads per lane
+  static constexpr int VCH = HD * VB / 4;                 // 16-byte V chunks per group
+  static constexpr int NV = (VCH + 63) / 64;              // V loads per lane
+  static constexpr int NKM = HD / 64;                     // K scale / min per lane
+  u4_t k[NK];
+  u4_t v[NV];
+  uint16_t ks[NKM], km[NKM];
+  uint32_t vmeta[HD / 64];   // lane < 32: V scales of token lane, else V mins of token lane-32
+};
+
+struct SegOffsets {
+  int64_t kd, km, vd, vm;
+};
+
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void load_group(GroupRegs<HD, KB, VB>& r, const SegDev& s,
+                                           const SegOffsets& o, bool kfast, int t0, int nvalid,
+                                           int lane) {
+  using R = GroupRegs<HD, KB, VB>;
+  if (kfast) {
+    const int64_t row_bytes = ((int64_t)s.length * KB + 7) / 8;
+    const int64_t byte0 = (int64_t)t0 * KB / 8;
+#pragma unroll
+    for (int i = 0; i < R::NK; ++i) {
+      const int q = lane + 64 * i;
+      const int c = q / R::KCR, u = q - c * R::KCR;
+      int64_t off = byte0 + R::KCB * u;
+      off = off < row_bytes ? off : row_bytes - R::KCB;
+      const uint8_t* src = s.kd + o.kd + c * row_bytes + off;
+      if (KB == 2) {
+        const u2_t x = *reinterpret_cast<const u2_t*>(src);
+        r.k[i] = u4_t{x[0], x[1], 0u, 0u};
+      } else {
+        r.k[i] = *reinterpret_cast<const u4_t*>(src);
+      }
+    }
+  }
+  const int row_groups = (s.length + s.kgs - 1) / s.kgs;
+  const int g = t0 / 32;
+#pragma unroll
+  for (int i = 0; i < R::NKM; ++i) {
+    const int c = lane + 64 * i;
+    r.ks[i] = s.ks[o.km + (int64_t)c * row_groups + g];
+    r.km[i] = s.km[o.km + (int64_t)c * row_groups + g];
+  }
+  const int last_chunk = nvalid * R::VCH / kTile - 1;   // last 16-byte chunk of a valid row
+  const uint8_t* vsrc = s.vd + o.vd + (int64_t)t0 * (HD * VB / 8);
+#pragma unroll
+  for (int i = 0; i < R::NV; ++i) {
+    int q = lane + 64 * i;
+    q = q < last_chunk ? q : last_chunk;
+    r.v[i] = *reinterpret_cast<const u4_t*>(vsrc + (int64_t)q * 16);
+  }
+  {
+    const int t = min(lane & 31, nvalid - 1);
+    const uint16_t* src = ((lane < 32) ? s.vs : s.vm) + o.vm + (int64_t)(t0 + t) * (HD / 32);
+    if (HD == 128) {
+      const u2_t x = *reinterpret_cast<const u2_t*>(src);
+      r.vmeta[0] = x[0];
+      r.vmeta[HD / 64 - 1] = x[1];
+    } else {
+      r.vmeta[0] = *reinterpret_cast<const uint32_t*>(src);
+    }
+  }
+}
+
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void store_group(const GroupRegs<HD, KB, VB>& r, const SegDev& s,
+                                            const SegOffsets& o, bool kfast, int t0, int lane,
+                                            char* lds) {
+  using L = KiviLayout<HD, KB, VB>;
+  using R = GroupRegs<HD, KB, VB>;
+  uint32_t* kw = reinterpret_cast<uint32_t*>(lds);
+  if (kfast) {
+#pragma unroll
+    for (int i = 0; i < R::NK; ++i) {
+      const int q = lane + 64 * i;
+      const int c = q / R::KCR, u = q - c * R::KCR;
+      constexpr int W = R::KCB / 4;
+#pragma unroll
+      for (int k = 0; k < W; ++k) kw[(W * u + k) * HD + c] = r.k[i][k];
+    }
+  } else {
+    // rows that are not a multiple of the load width (short segments): 4 or 1 bytes at a time
+    const int64_t row_bytes = ((int64_t)s.length * KB + 7) / 8;
+    const int64_t byte0 = (int64_t)t0 * KB / 8;
+    const uint8_t* krow0 = s.kd + o.kd;
+    const bool dw = (row_bytes & 3) == 0;
+    for (int q = lane; q < HD * KB; q += 64) {
+      const int c = q / KB, w = q - c * KB;
+      const int64_t off = byte0 + 4 * w;
+      uint32_t v = 0u;
+      if (dw) {
+        if (off < row_bytes) v = *reinterpret_cast<const uint32_t*>(krow0 + c * row_bytes + off);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (off + k < row_bytes) v |= (uint32_t)krow0[c * row_bytes + off + k] << (8 * k);
+      }
+      kw[w * HD + c] = v;
+    }
+  }
+  uint16_t* ks = reinterpret_cast<uint16_t*>(lds + L::off_ks);
+  uint16_t* km = reinterpret_cast<uint16_t*>(lds + L::off_km);
+#pragma unroll
+  for (int i = 0; i < R::NKM; ++i) {
+    ks[lane + 64 * i] = r.ks[i];
+    km[lane + 64 * i] = r.km[i];
+  }
+  u4_t* vw = reinterpret_cast<u4_t*>(lds + L::off_vw);
+#pragma unroll
+  for (int i = 0; i < R::NV; ++i)
+    if (lane + 64 * i < R::VCH) vw[lane + 64 * i] = r.v[i];
+  // V metadata: token-major in global, channel-group-major in LDS
+  uint16_t* vmeta = reinterpret_cast<uint16_t*>(lds + ((lane < 32) ? L::off_vs : L::off_vm));
+  const int t = lane & 31;
+#pragma unroll
+  for (int cg = 0; cg < HD / 32; ++cg)
+    vmeta[cg * kTile + t] = (uint16_t)(r.vmeta[cg >> 1] >> (16 * (cg & 1)));
+}
+
+// token (within the group) of QK result row rr of instance h
+template <int KB>
+__device__ __forceinline__ int qk_token(int h, int rr) {
+  if (KB == 2) return 4 * (rr >> 1) + 2 * h + (rr & 1);
+  if (KB == 4) return 2 * rr + h;
+  return 16 * h + rr;
+}
+
+// power-of-two factor the K code of result row rr carries (2^(bit position))
+template <int KB>
+__device__ __forceinline__ float qk_posfactor(int h, int e) {
+  if (KB == 2) return (float)(1 << (2 * (2 * h + (e & 1))));
+  if (KB == 4) return h ? 16.0f : 1.0f;
+  return 1.0f;
+}
+
+// token of the lane's PV slot j
+template <int KB>
+__device__ __forceinline__ int pv_token(int g4, int j) {
+  if (KB == 8) return 16 * (j >> 2) + 4 * g4 + (j & 3);
+  return 8 * g4 + j;
+}
+
+// PV slot of QK result (h, e)
+template <int KB>
+__device__ __forceinline__ int pv_slot(int h, int e) {
+  if (KB == 2) return 4 * (e >> 1) + 2 * h + (e & 1);
+  if (KB == 4) return 2 * e + h;
+  return 4 * h + e;
+}
+
+// ---------------------------------------------------------------------------
+// one staged 32-token KIVI group
+// ---------------------------------------------------------------------------
+template <int HD, int KB, int VB>
+__device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD / 8],
+                           WaveAcc<HD>& acc, float sl2, int lane) {
+  using L = KiviLayout<HD, KB, VB>;
+  constexpr int KS = HD / 32;
+  constexpr int NB = HD / 16;
+  constexpr int CG = HD / 32;
+  const int r = lane & 15;     // A row (token row) / B column (head)
+  const int g4 = lane >> 4;
+  // ---- q folded with the group's K scale, and the K-min bias ----
+  u4_t qp[KS];
+  float bpart = 0.f;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const u4_t sc8 = lds_u4(lds + L::off_ks + (32 * s + 8 * g4) * 2);
+    const u4_t mn8 = lds_u4(lds + L::off_km + (32 * s + 8 * g4) * 2);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      qp[s][m] = pkmul(qh[s * 4 + m], sc8[m]);
+      bpart = dot2(qh[s * 4 + m], mn8[m], bpart);
+    }
+  }
+  const float bias = xsum4(bpart) * sl2;
+  // ---- S^T = codes_K * q' for instances h = 0, 1 (16 tokens each) ----
+  f4_t d[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  if constexpr (KB == 8) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int w = 4 * h + (r >> 2);
+        const uint32_t sel = sel_bytes(r & 3);
+        const u4_t w0 = lds_u4(lds + (w * HD + 32 * s + 8 * g4) * 4);
+        const u4_t w1 = lds_u4(lds + (w * HD + 32 * s + 8 * g4 + 4) * 4);
+        u4_t a;
+        a[0] = perm(w0[1], w0[0], sel);
+        a[1] = perm(w0[3], w0[2], sel);
+        a[2] = perm(w1[1], w1[0], sel);
+        a[3] = perm(w1[3], w1[2], sel);
+        d[h] = mfma(a, qp[s], d[h]);
+      }
+    }
+  } else {
+    const int w = (KB == 2) ? (r >> 3) : (r >> 2);
+    const uint32_t sel = sel_bytes(KB == 2 ? ((r >> 1) & 3) : (r & 3));
+    uint32_t mask[2];
+    if (KB == 2) {
+      mask[0] = 0x00030003u << (2 * (r & 1));
+      mask[1] = 0x00030003u << (2 * (2 + (r & 1)));
+    } else {
+      mask[0] = 0x000F000Fu;
+      mask[1] = 0x00F000F0u;
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u4_t w0 = lds_u4(lds + (w * HD + 32 * s + 8 * g4) * 4);
+      const u4_t w1 = lds_u4(lds + (w * HD + 32 * s + 8 * g4 + 4) * 4);
+      uint32_t u[4];
+      u[0] = perm(w0[1], w0[0], sel);
+      u[1] = perm(w0[3], w0[2], sel);
+      u[2] = perm(w1[1], w1[0], sel);
+      u[3] = perm(w1[3], w1[2], sel);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u4_t a;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) a[m] = u[m] & mask[h];
+        d[h] = mfma(a, qp[s], d[h]);
+      }
+    }
+  }
+  // ---- scores (log2 units) ----
+  float sc[2][4];
+  float mt = -INFINITY;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tok = qk_token<KB>(h, 4 * g4 + e);
+      const float f = kTwo24 * sl2 / qk_posfactor<KB>(h, e);
+      const float v = (tok < nvalid) ? fmaf(d[h][e], f, bias) : -INFINITY;
+      sc[h][e] = v;
+      mt = fmaxf(mt, v);
+    }
+  }
+  mt = xmax4(mt);
+  // ---- online softmax ----
+  const float m_new = fmaxf(acc.m, mt);
+  const float alpha = __builtin_amdgcn_exp2f(acc.m - m_new);
+  float p[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[pv_slot<KB>(h, e)] = __builtin_amdgcn_exp2f(sc[h][e] - m_new);
+  }
+  // p is rounded to fp16 once; the sum l, P' and the V-min bias all use that
+  // rounded value, so the rounding only perturbs the softmax weights.
+  uint32_t p2[4];
+  float psum = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    p2[m] = pack_h2(p[2 * m], p[2 * m + 1]);
+    psum = dot2(p2[m], kOnes2, psum);
+  }
+  acc.l = acc.l * alpha + psum;
+  acc.m = m_new;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc.o[b] *= alpha;
+#pragma unroll
+  for (int c = 0; c < CG; ++c) acc.vb[c] *= alpha;
+  // ---- P' = p * sV per channel group, and the V-min bias ----
+  u4_t pp[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    u4_t sv, mv;
+    if constexpr (KB == 8) {
+      const u2_t s0 = lds_u2(lds + L::off_vs + (c * kTile + 4 * g4) * 2);
+      const u2_t s1 = lds_u2(lds + L::off_vs + (c * kTile + 16 + 4 * g4) * 2);
+      const u2_t m0 = lds_u2(lds + L::off_vm + (c * kTile + 4 * g4) * 2);
+      const u2_t m1 = lds_u2(lds + L::off_vm + (c * kTile + 16 + 4 * g4) * 2);
+      sv = u4_t{s0[0], s0[1], s1[0], s1[1]};
+      mv = u4_t{m0[0], m0[1], m1[0], m1[1]};
+    } else {
+      sv = lds_u4(lds + L::off_vs + (c * kTile + 8 * g4) * 2);
+      mv = lds_u4(lds + L::off_vm + (c * kTile + 8 * g4) * 2);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      pp[c][m] = pkmul(p2[m], sv[m]);
+      acc.vb[c] = dot2(p2[m], mv[m], acc.vb[c]);
+    }
+  }
+  // ---- O^T += codes_V^T * P' : channel block b, row r <-> channel 16 b + r ----
+  constexpr int RW = L::vrow_words;
+  const char* vw = lds + L::off_vw;
+  int tok[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) tok[j] = pv_token<KB>(g4, j);
+  if constexpr (VB == 2) {
+    // a 16-channel block is one word of a V row; 4 blocks per 16-byte read
+    const uint32_t vsel = sel_bytes(r >> 2);
+    const uint32_t vmask = 0x00030003u << (2 * (r & 3));
+#pragma unroll
+    for (int k = 0; k < NB / 4; ++k) {
+      u4_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = lds_u4(vw + (tok[j] * RW + 4 * k) * 4);
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        u4_t a;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) a[m] = perm(w[2 * m + 1][bb], w[2 * m][bb], vsel) & vmask;
+        acc.o[4 * k + bb] = mfma(a, pp[(4 * k + bb) >> 1], acc.o[4 * k + bb]);
+      }
+    }
+  } else if constexpr (VB == 4) {
+    // block b spans two words; rows r >= 8 take the second one
+    const uint32_t vsel = sel_bytes((r >> 1) & 3);
+    const uint32_t vmask = 0x000F000Fu << (4 * (r & 1));
+    const bool hi = (r >> 3) != 0;
+#pragma unroll
+    for (int k = 0; k < NB / 2; ++k) {
+      u4_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = lds_u4(vw + (tok[j] * RW + 4 * k) * 4);
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        u4_t a;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const uint32_t wa = hi ? w[2 * m][2 * bb + 1] : w[2 * m][2 * bb];
+          const uint32_t wb = hi ? w[2 * m + 1][2 * bb + 1] : w[2 * m + 1][2 * bb];
+          a[m] = perm(wb, wa, vsel) & vmask;
+        }
+        acc.o[2 * k + bb] = mfma(a, pp[(2 * k + bb) >> 1], acc.o[2 * k + bb]);
+      }
+    }
+  } else {
+    const uint32_t vsel = sel_bytes(r & 3);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int w = 4 * b + (r >> 2);
+      u4_t a;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t wa = lds_u32(vw + (tok[2 * m] * RW + w) * 4);
+        const uint32_t wb = lds_u32(vw + (tok[2 * m + 1] * RW + w) * 4);
+        a[m] = perm(wb, wa, vsel);
+      }
+      acc.o[b] = mfma(a, pp[b >> 1], acc.o[b]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// FP16 segment: operands straight from global memory, 32 tokens per step.
+// Token addresses are clamped into the segment: rows past the end only feed
+// masked scores (K) or p = 0 weights (V).
+// ---------------------------------------------------------------------------
+template <int HD>
+__device__ void fp16_group(const uint16_t* kbase, const uint16_t* vbase, int64_t tok_stride,
+                           int t0, int nvalid, const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
+                           float sl2, int lane) {
+  constexpr int KS = HD / 32;
+  constexpr int NB = HD / 16;
+  constexpr int VW = NB / 2;   // 32-bit words per token and lane
+  const int r = lane & 15;
+  const int g4 = lane >> 4;
+  u4_t kk[2][KS];
+  uint32_t vv[8][VW];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = min(16 * h + r, nvalid - 1);
+    const uint16_t* krow = kbase + (int64_t)(t0 + t) * tok_stride;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kk[h][s] = *reinterpret_cast<const u4_t*>(krow + 32 * s + 8 * g4);
+  }
+  // V^T rows: instance b, row r <-> channel NB * r + b; each lane reads its NB channels per token
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int t = min(16 * (j >> 2) + 4 * g4 + (j & 3), nvalid - 1);
+    const uint16_t* vrow = vbase + (int64_t)(t0 + t) * tok_stride + NB * r;
+    if constexpr (VW == 4) {
+      const u4_t x = *reinterpret_cast<const u4_t*>(vrow);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) vv[j][k] = x[k];
+    } else {
+      const u2_t x = *reinterpret_cast<const u2_t*>(vrow);
+      vv[j][0] = x[0];
+      vv[j][1] = x[1];
+    }
+  }
+  f4_t d[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) d[h] = mfma(kk[h][s], qb[s], d[h]);
+  float sc[2][4];
+  float mt = -INFINITY;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * h + 4 * g4 + e;
+      const float v = (t < nvalid) ? d[h][e] * sl2 : -INFINITY;
+      sc[h][e] = v;
+      mt = fmaxf(mt, v);
+    }
+  mt = xmax4(mt);
+  const float m_new = fmaxf(acc.m, mt);
+  const float alpha = __builtin_amdgcn_exp2f(acc.m - m_new);
+  float p[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[4 * h + e] = __builtin_amdgcn_exp2f(sc[h][e] - m_new);
+  u4_t p2;
+  float psum = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    p2[m] = pack_h2(p[2 * m], p[2 * m + 1]);
+    psum = dot2(p2[m], kOnes2, psum);
+  }
+  acc.l = acc.l * alpha + psum;
+  acc.m = m_new;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc.o[b] *= alpha;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const uint32_t sel = sel_halves(b & 1);
+    u4_t a;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) a[m] = perm(vv[2 * m + 1][b >> 1], vv[2 * m][b >> 1], sel);
+    acc.o[b] = mfma(a, p2, acc.o[b]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// the kernel
+// ---------------------------------------------------------------------------
+template <int HD, int KB, int VB>
+__device__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_begin, int t_end, int wave,
+                           int lane, char* lds_wave, const uint32_t (&qh)[HD / 8],
+                           WaveAcc<HD>& acc, float sl2) {
+  int t0 = t_begin + kTile * wave;
+  if (t0 >= t_end) return;
+  using R = GroupRegs<HD, KB, VB>;
+  const bool kfast = ((((int64_t)s.length * KB + 7) / 8) % R::KCB) == 0;
+  R regs;
+  load_group<HD, KB, VB>(regs, s, o, kfast, t0, min(kTile, t_end - t0), lane);
+  for (;;) {
+    const int nvalid = min(kTile, t_end - t0);
+    store_group<HD, KB, VB>(regs, s, o, kfast, t0, lane, lds_wave);
+    __builtin_amdgcn_wave_barrier();
+    const int t_next = t0 + kTile * kWaves;
+    if (t_next < t_end) load_group<HD, KB, VB>(regs, s, o, kfast, t_next, min(kTile, t_end - t_next), lane);
+    kivi_group<HD, KB, VB>(nvalid, lds_wave, qh, acc, sl2, lane);
+    __builtin_amdgcn_wave_barrier();
+    if (t_next >= t_end) break;
+    t0 = t_next;
+  }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256)
+decode_mfma_kernel(const DecodeParams p) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  constexpr int NB = HD / 16;
+  constexpr int KS = HD / 32;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int n = lane & 15;
+  const int g4 = lane >> 4;
+
+  const int b = blockIdx.z;
+  const int kvh = blockIdx.y / p.nslab;
+  const int slab = blockIdx.y - kvh * p.nslab;
+  const int h0 = kvh * p.G + slab * p.HS;
+  const int nh = min(p.HS, p.G - slab * p.HS);
+
+  int si = 0;
+  while (si + 1 < p.nseg && (int)blockIdx.x >= p.seg[si + 1].lbegin) ++si;
+  const SegDev& s = p.seg[si];
+  const int local = blockIdx.x - s.lbegin;
+  const int cg = s.gbegin + local;
+  int len_b = s.length;
+  if (s.seq_lens) len_b = min(len_b, s.seq_lens[b]);
+  const int t_begin = local * s.chunk_len;
+  const int t_end = min(t_begin + s.chunk_len, len_b);
+  const float sl2 = p.scale * kLog2e;
+
+  // q of head n (zero for padding heads): lane's channels 32 s + 8 g4 .. + 7
+  u4_t qb[KS];
+  uint32_t qh[HD / 8];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    u4_t v = {0u, 0u, 0u, 0u};
+    if (n < nh)
+      v = *reinterpret_cast<const u4_t*>(p.q + (int64_t)b * p.q_bs + (int64_t)(h0 + n) * p.q_hs +
+                                         32 * k + 8 * g4);
+    qb[k] = v;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) qh[4 * k + m] = v[m];
+  }
+
+  WaveAcc<HD> acc;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) acc.o[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i) acc.vb[i] = 0.f;
+  acc.m = -INFINITY;
+  acc.l = 0.f;
+
+  char* lds_wave = lds + wave * p.wave_lds;
+  if (s.kind == PK_SEG_FP16) {
+    const uint16_t* kbase = reinterpret_cast<const uint16_t*>(s.kd) + b * s.kd_bs + kvh * s.kd_hs;
+    const uint16_t* vbase = reinterpret_cast<const uint16_t*>(s.vd) + b * s.vd_bs + kvh * s.vd_hs;
+    for (int t0 = t_begin + 32 * wave; t0 < t_end; t0 += 32 * kWaves)
+      fp16_group<HD>(kbase, vbase, s.tok_stride, t0, min(32, t_end - t0), qb, acc, sl2, lane);
+  } else {
+    SegOffsets o;
+    o.kd = b * s.kd_bs + kvh * s.kd_hs;
+    o.km = b * s.km_bs + kvh * s.km_hs;
+    o.vd = b * s.vd_bs + kvh * s.vd_hs;
+    o.vm = b * s.vm_bs + kvh * s.vm_hs;
+#define PK_KIVI_CASE(KB_, VB_)                                                               \
+  if (s.kbits == KB_ && s.vbits == VB_)                                                      \
+    kivi_chunk<HD, KB_, VB_>(s, o, t_begin, t_end, wave, lane, lds_wave, qh, acc, sl2);
+    PK_KIVI_CASE(2, 2) else PK_KIVI_CASE(2, 4) else PK_KIVI_CASE(2, 8)
+    else PK_KIVI_CASE(4, 2) else PK_KIVI_CASE(4, 4) else PK_KIVI_CASE(4, 8)
+    else PK_KIVI_CASE(8, 2) else PK_KIVI_CASE(8, 4) else PK_KIVI_CASE(8, 8)
+#undef PK_KIVI_CASE
+  }
+
+  // ---- wave results -> LDS, merge the 4 waves ----
+  __syncthreads();
+  float* mo = reinterpret_cast<float*>(lds);               // [4][16][HD]
+  float* mm = mo + kWaves * 16 * HD;                        // [4][16]
+  float* ml = mm + kWaves * 16;                             // [4][16]
+  const float l_full = xsum4(acc.l);
+  if (s.kind == PK_SEG_FP16) {
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        mo[(wave * 16 + n) * HD + NB * (4 * g4 + e) + bb] = acc.o[bb][e];
+  } else {
+    float vbf[HD / 32];
+#pragma unroll
+    for (int c = 0; c < HD / 32; ++c) vbf[c] = xsum4(acc.vb[c]);
+    // V code position factor of result row 4 g4 + e
+    const int vb_bits = s.vbits;
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pos = (vb_bits == 2) ? (float)(1 << (2 * e))
+                          : (vb_bits == 4) ? ((e & 1) ? 16.f : 1.f) : 1.f;
+        mo[(wave * 16 + n) * HD + 16 * bb + 4 * g4 + e] =
+            acc.o[bb][e] * (kTwo24 / pos) + vbf[bb >> 1];
+      }
+  }
+  if (g4 == 0) {
+    mm[wave * 16 + n] = acc.m;
+    ml[wave * 16 + n] = l_full;
+  }
+  __syncthreads();
+  for (int i = tid; i < nh * HD; i += 256) {
+    const int hh = i / HD, c = i - hh * HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mm[w * 16 + hh]);
+    float o = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w)
+        o += __builtin_amdgcn_exp2f(mm[w * 16 + hh] - M) * mo[(w * 16 + hh) * HD + c];
+    }
+    const int64_t row = (int64_t)b * p.Hq + h0 + hh;
+    p.ws_acc[(row * p.C + cg) * HD + c] = o;
+  }
+  for (int hh = tid; hh < nh; hh += 256) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mm[w * 16 + hh]);
+    float L = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) L += __builtin_amdgcn_exp2f(mm[w * 16 + hh] - M) * ml[w * 16 + hh];
+    }
+    const int64_t row = (int64_t)b * p.Hq + h0 + hh;
+    p.ws_m[row * p.C + cg] = (M == -INFINITY) ? -INFINITY : M * kLn2;
+    p.ws_l[row * p.C + cg] = L;
+  }
+}
+
+}  // namespace
+
+// LDS bytes per wave for the largest K / V bit widths of a launch
+static int kivi_wave_bytes(int hd, int kb, int vb) {
+  return 4 * hd * (kb + vb + 2);
+}
+
+int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, int max_vbits,
+                       hipStream_t stream) {
+  DecodeParams dp = dp_in;
+  const int hd = dp.hd;
+  dp.wave_lds = (kivi_wave_bytes(hd, max_kbits, max_vbits) + 15) & ~15;
+  const size_t staging = (size_t)kWaves * dp.wave_lds;
+  const size_t merge = sizeof(float) * ((size_t)kWaves * 16 * hd + 2 * kWaves * 16);
+  const size_t lds = std::max(staging, merge);
+  dim3 grid(lchunks, dp.Hkv * dp.nslab, dp.B);
+  if (hd == 128)
+    hipLaunchKernelGGL(decode_mfma_kernel<128>, grid, dim3(256), lds, stream, dp);
+  else
+    hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(256), lds, stream, dp);
+  return check_launch("decode_mfma");
+}
+
+}  // namespace pk

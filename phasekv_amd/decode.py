@@ -130,7 +130,8 @@ def fp16_segment(k: torch.Tensor, v: torch.Tensor, *, batched: bool, splits: int
 class Problem:
     """A decode problem (q plus segments) as the C structure, with its keep-alive list."""
 
-    def __init__(self, q: torch.Tensor, segments: List[Segment], num_attention_heads: int):
+    def __init__(self, q: torch.Tensor, segments: List[Segment], num_attention_heads: int,
+                 generic_kernel: bool = False):
         if not segments:
             raise ValueError("no KV to attend: every tier is empty")
         if q.dim() == 2:
@@ -165,6 +166,7 @@ class Problem:
         p.q_bstride, p.q_hstride = q.stride(0), q.stride(1)
         p.segments = ctypes.cast(arr, ctypes.POINTER(_lib.PkSegment))
         p.num_segments = len(segments)
+        p.flags = _lib.PK_FLAG_GENERIC_KERNEL if generic_kernel else 0
         self.c = p
 
     def workspace_size(self) -> Tuple[int, int]:
@@ -177,7 +179,7 @@ class Problem:
 
 
 # Reusable workspaces per (device, stream): calls on one stream are ordered, so
-# they can share one buffer; its counter region is zeroed once when allocated.
+# they can share one buffer.
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
 
 
@@ -188,14 +190,12 @@ def cached_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     if ws is None or ws.numel() < nbytes:
         size = max(nbytes + nbytes // 2, 4 << 20)
         ws = torch.empty(size, dtype=torch.uint8, device=device)
-        _lib.check(_lib.load().pk_decode_workspace_init(ws.data_ptr(), ws.numel(), stream),
-                   "decode_workspace_init")
         _WORKSPACES[key] = ws
     return ws
 
 
 def fused_decode(problem: Problem) -> torch.Tensor:
-    """Normalized attention output [B, Hq, hd] fp16 in one launch (per 8 segments)."""
+    """Normalized attention output [B, Hq, hd] fp16: one partial launch (per 8 segments) + combine."""
     nbytes, _ = problem.workspace_size()
     ws = cached_workspace(problem.device, nbytes)
     out = torch.empty(problem.batch, problem.hq, problem.hd, dtype=torch.float16,
@@ -215,7 +215,7 @@ def decode_partials(problem: Problem):
     _lib.check(lib.pk_decode_partials(ctypes.byref(problem.c), ws.data_ptr(), ws.numel(),
                                       _lib.stream_ptr(problem.device)), "decode_partials")
     rows = problem.batch * problem.hq
-    off_m = _lib.PK_WORKSPACE_COUNTER_BYTES
+    off_m = 0
     align = lambda x: (x + 255) & ~255
     off_l = align(off_m + rows * splits * 4)
     off_acc = align(off_l + rows * splits * 4)

@@ -1,9 +1,10 @@
 """HIP decode attention vs the oracle on identical inputs.
 
-Bar (from the task): max-abs 2e-3 and relative 1e-2 against the float64
-oracle of the reference semantics; the reference's own CUDA test used
-atol 3e-4 / rtol 1e-3 (tests/test_phasekv_launch_config.py:79), which the
-single-segment cases also meet.
+Bar: max-abs 2e-3 and relative 1e-2 against the float64 oracle of the
+reference semantics.  (The reference's CUDA test used atol 3e-4 / rtol 1e-3
+for its fp32 Triton kernel, tests/test_phasekv_launch_config.py:79; the MFMA
+kernel rounds q * K-scale and p * V-scale to fp16 operands, which stays inside
+2e-3 but not always inside 3e-4 on tiny 8-bit segments.)
 """
 import math
 from dataclasses import replace
@@ -53,10 +54,10 @@ def test_kivi_layer_partial_matches_dense_reference(gpu, length, heads, dim, kb,
     expected = acc_ref / l_ref[:, None]
     for options in ({}, {"num_splits": 8, "block_n": 64, "num_warps": 4}, {"num_splits": 3}):
         m, total, acc = _kivi_layer_partial(q.to(gpu), k, v, heads, **options)
-        _close(acc / total[:, None], expected, atol=3e-4, rtol=1e-3)
-        # m is the max score: the unnormalized pair rescales to the oracle's
+        _close(acc / total[:, None], expected)
+        # m is the max score: the unnormalized (m, l) pair rescales to the oracle's
         w = torch.exp(m.cpu().double() - torch.from_numpy(m_ref))
-        np.testing.assert_allclose((total.cpu().double() * w).numpy(), l_ref, rtol=1e-4)
+        np.testing.assert_allclose((total.cpu().double() * w).numpy(), l_ref, rtol=2e-3)
 
 
 def _make_tiers(gpu, g, hkv, hd, prompt, pbits, colds, cbits, hot, cap_extra=8, ext=()):
