@@ -1,6 +1,7 @@
 """Benchmark of the PhaseKV Stage-B decode attention on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-sweep] [--no-cpu]
+                    [--no-dense]
 
 A step is one decode-attention call (one layer, one query token) over the
 packed prompt tier, the cold tier and the FP16 hot window of the workload.
@@ -11,7 +12,8 @@ algorithmic HBM bandwidth (packed K/V codes + fp16 scale/min + fp16 hot
 window + q + output per step) divided by the measured step time.
 
 Prints ONE JSON line (rank 0).  Extra fields: ``us_per_step``, the FP16 dense
-GQA-aware comparator on the same tokens, and a context sweep (C3).
+GQA-aware comparator on the same tokens, and ``sweep``: the same measurement
+for the context sweep (C3) and the batched configurations (C4, C5).
 """
 from __future__ import annotations
 
@@ -79,22 +81,26 @@ def _bench_config(cfg, device, steps, warmup, stream, with_dense=True):
     res["frac"] = res["gbs"] / HBM_PEAK_GBS
     del tiers, fns
     if with_dense:
-        # uncompressed fp16 K/V of the same tokens, GQA-aware (no expanded copies)
-        k = torch.cat([t for t in wl.dense_k if t is not None], dim=2).to(device)
-        v = torch.cat([t for t in wl.dense_v if t is not None], dim=2).to(device)
+        # uncompressed fp16 K/V of the same tokens (prompt rows at their ragged lengths),
+        # read by the same GQA-aware kernel as the hot window: no expanded copies
+        from phasekv_amd import decode as dec
+        dense = [(k.to(device), v.to(device)) for k, v in zip(wl.dense_k, wl.dense_v)
+                 if k is not None]
         dbytes = workloads.fp16_dense_bytes(cfg, wl.prompt_lens_list if cfg.ragged_min else None)
         dcopies = _copies_for(dbytes, 64)
-        ks = [k] + [k.clone() for _ in range(dcopies - 1)]
-        vs = [v] + [v.clone() for _ in range(dcopies - 1)]
-        if cfg.batch == 1:
-            dfns = [lambda a=a, b=b: dense_fp16_decode(q[0], a[0], b[0], cfg.hq) for a, b in zip(ks, vs)]
-        else:
-            dfns = [lambda a=a, b=b: dense_fp16_decode(q, a, b, cfg.hq) for a, b in zip(ks, vs)]
+        sets = [dense] + [[(k.clone(), v.clone()) for k, v in dense] for _ in range(dcopies - 1)]
+        probs = []
+        for kv in sets:
+            segs = [dec.fp16_segment(k, v, batched=True,
+                                     seq_lens=wl.prompt_lens if (i == 0 and cfg.ragged_min) else None)
+                    for i, (k, v) in enumerate(kv)]
+            probs.append(dec.Problem(q, segs, cfg.hq))
+        dfns = [lambda pr=pr: dec.fused_decode(pr) for pr in probs]
         dsec = _time_graph(dfns, steps, warmup, stream)
         res["fp16_dense_us"] = dsec * 1e6
         res["fp16_dense_gbs"] = dbytes / dsec / 1e9
         res["speedup_vs_fp16"] = dsec / sec
-        del ks, vs, dfns, k, v
+        del sets, probs, dfns, dense
     torch.cuda.empty_cache()
     return res, wl
 
@@ -142,6 +148,7 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-dense", action="store_true", help="skip the FP16 dense comparator")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the decode path "
@@ -156,13 +163,15 @@ def main() -> int:
     stream = torch.cuda.Stream(device)
     cfg = workloads.CONFIGS[args.config]
     _log(f"bench: {cfg} steps={args.steps} warmup={args.warmup}")
-    main_res, _ = _bench_config(cfg, device, args.steps, args.warmup, stream)
+    main_res, _ = _bench_config(cfg, device, args.steps, args.warmup, stream,
+                                with_dense=not args.no_dense)
     _log(f"bench: {cfg.name} {main_res}")
     sweep = []
     if not args.no_sweep:
-        for name in ("C3-4K", "C3-8K", "C3-16K", "C3-32K"):
-            r, _ = _bench_config(workloads.CONFIGS[name], device, min(args.steps, 256),
-                                 min(args.warmup, 256), stream)
+        for name in ("C3-4K", "C3-8K", "C3-16K", "C3-32K", "C4", "C5"):
+            steps = min(args.steps, 256) if workloads.CONFIGS[name].batch == 1 else 32
+            r, _ = _bench_config(workloads.CONFIGS[name], device, steps, min(args.warmup, steps),
+                                 stream, with_dense=not args.no_dense)
             _log(f"bench: {name} {r}")
             sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
     cpu = None

@@ -109,20 +109,47 @@ template <int HD>
 struct WaveAcc {
   f4_t o[HD / 16];     // O^T blocks: rows 4*g4 + e of channel block b, column = head
   float vb[HD / 32];   // sum_t p * mV  (this lane's tokens)
-  float m;             // running max, log2 units, same in the 4 lane groups
+  float m;             // reference max of p = 2^(s - m), log2 units, same in the 4 lane groups
+  float mx;            // true running max of the scores
   float l;             // sum_t p (this lane's tokens)
 };
 
+// The reference max only moves when a group's max exceeds it by more than
+// kLazyLog2, so p = 2^(s - m) <= 2^kLazyLog2 stays well inside fp16 and the
+// accumulators are rescaled only when some head of the wave needs it (a
+// wave-uniform branch), instead of every group.  Returns the reference max to
+// use for this group's p.
+constexpr float kLazyLog2 = 8.0f;
+
+template <int HD>
+__device__ __forceinline__ float lazy_rescale(WaveAcc<HD>& acc, float mt) {
+  acc.mx = fmaxf(acc.mx, mt);
+  const bool grow = mt > acc.m + kLazyLog2;
+  if (__any(grow)) {
+    const float m_new = grow ? mt : acc.m;
+    const float alpha = __builtin_amdgcn_exp2f(acc.m - m_new);
+    acc.m = m_new;
+    acc.l *= alpha;
+#pragma unroll
+    for (int b = 0; b < HD / 16; ++b) acc.o[b] *= alpha;
+#pragma unroll
+    for (int c = 0; c < HD / 32; ++c) acc.vb[c] *= alpha;
+  }
+  return acc.m;
+}
+
 // ---------------------------------------------------------------------------
 // per-wave LDS staging of one 32-token KIVI group
-//   Kw  uint32 [KB][HD]         the group's K bytes of every channel row
+//   Kw  uint32 [KB][HD + 8]     the group's K bytes of every channel row (rows padded
+//                               by 8 words so neighbouring words land in other banks)
 //   Ks, Km  fp16 [HD]           K scale / min of the group
 //   Vw  uint32 [32][HD*VB/32]   the group's V rows
 //   Vs, Vm  fp16 [HD/32][32]    V scale / min, channel group major
 // ---------------------------------------------------------------------------
 template <int HD, int KB, int VB>
 struct KiviLayout {
-  static constexpr int kw_bytes = KB * HD * 4;
+  static constexpr int kw_row = HD + 8;                   // words per Kw row
+  static constexpr int kw_bytes = KB * kw_row * 4;
   static constexpr int vrow_words = HD * VB / 32;
   static constexpr int vrow_bytes = HD * VB / 8;
   static constexpr int vw_bytes = kTile * vrow_bytes;
@@ -222,7 +249,7 @@ __device__ __forceinline__ void store_group(const GroupRegs<HD, KB, VB>& r, cons
       const int c = q / R::KCR, u = q - c * R::KCR;
       constexpr int W = R::KCB / 4;
 #pragma unroll
-      for (int k = 0; k < W; ++k) kw[(W * u + k) * HD + c] = r.k[i][k];
+      for (int k = 0; k < W; ++k) kw[(W * u + k) * L::kw_row + c] = r.k[i][k];
     }
   } else {
     // rows that are not a multiple of the load width (short segments): 4 or 1 bytes at a time
@@ -241,7 +268,7 @@ __device__ __forceinline__ void store_group(const GroupRegs<HD, KB, VB>& r, cons
         for (int k = 0; k < 4; ++k)
           if (off + k < row_bytes) v |= (uint32_t)krow0[c * row_bytes + off + k] << (8 * k);
       }
-      kw[w * HD + c] = v;
+      kw[w * L::kw_row + c] = v;
     }
   }
   uint16_t* ks = reinterpret_cast<uint16_t*>(lds + L::off_ks);
@@ -297,7 +324,7 @@ __device__ __forceinline__ int pv_slot(int h, int e) {
 // ---------------------------------------------------------------------------
 // one staged 32-token KIVI group
 // ---------------------------------------------------------------------------
-template <int HD, int KB, int VB>
+template <int HD, int KB, int VB, bool FULL>
 __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD / 8],
                            WaveAcc<HD>& acc, float sl2, int lane) {
   using L = KiviLayout<HD, KB, VB>;
@@ -329,8 +356,8 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
       for (int h = 0; h < 2; ++h) {
         const int w = 4 * h + (r >> 2);
         const uint32_t sel = sel_bytes(r & 3);
-        const u4_t w0 = lds_u4(lds + (w * HD + 32 * s + 8 * g4) * 4);
-        const u4_t w1 = lds_u4(lds + (w * HD + 32 * s + 8 * g4 + 4) * 4);
+        const u4_t w0 = lds_u4(lds + (w * L::kw_row + 32 * s + 8 * g4) * 4);
+        const u4_t w1 = lds_u4(lds + (w * L::kw_row + 32 * s + 8 * g4 + 4) * 4);
         u4_t a;
         a[0] = perm(w0[1], w0[0], sel);
         a[1] = perm(w0[3], w0[2], sel);
@@ -352,8 +379,8 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
     }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const u4_t w0 = lds_u4(lds + (w * HD + 32 * s + 8 * g4) * 4);
-      const u4_t w1 = lds_u4(lds + (w * HD + 32 * s + 8 * g4 + 4) * 4);
+      const u4_t w0 = lds_u4(lds + (w * L::kw_row + 32 * s + 8 * g4) * 4);
+      const u4_t w1 = lds_u4(lds + (w * L::kw_row + 32 * s + 8 * g4 + 4) * 4);
       uint32_t u[4];
       u[0] = perm(w0[1], w0[0], sel);
       u[1] = perm(w0[3], w0[2], sel);
@@ -377,15 +404,14 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
     for (int e = 0; e < 4; ++e) {
       const int tok = qk_token<KB>(h, 4 * g4 + e);
       const float f = kTwo24 * sl2 / qk_posfactor<KB>(h, e);
-      const float v = (tok < nvalid) ? fmaf(d[h][e], f, bias) : -INFINITY;
+      const float v = (FULL || tok < nvalid) ? fmaf(d[h][e], f, bias) : -INFINITY;
       sc[h][e] = v;
       mt = fmaxf(mt, v);
     }
   }
   mt = xmax4(mt);
-  // ---- online softmax ----
-  const float m_new = fmaxf(acc.m, mt);
-  const float alpha = __builtin_amdgcn_exp2f(acc.m - m_new);
+  // ---- online softmax with a lagging reference max ----
+  const float m_new = lazy_rescale(acc, mt);
   float p[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -401,12 +427,7 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
     p2[m] = pack_h2(p[2 * m], p[2 * m + 1]);
     psum = dot2(p2[m], kOnes2, psum);
   }
-  acc.l = acc.l * alpha + psum;
-  acc.m = m_new;
-#pragma unroll
-  for (int b = 0; b < NB; ++b) acc.o[b] *= alpha;
-#pragma unroll
-  for (int c = 0; c < CG; ++c) acc.vb[c] *= alpha;
+  acc.l += psum;
   // ---- P' = p * sV per channel group, and the V-min bias ----
   u4_t pp[CG];
 #pragma unroll
@@ -546,8 +567,7 @@ __device__ void fp16_group(const uint16_t* kbase, const uint16_t* vbase, int64_t
       mt = fmaxf(mt, v);
     }
   mt = xmax4(mt);
-  const float m_new = fmaxf(acc.m, mt);
-  const float alpha = __builtin_amdgcn_exp2f(acc.m - m_new);
+  const float m_new = lazy_rescale(acc, mt);
   float p[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
@@ -560,10 +580,7 @@ __device__ void fp16_group(const uint16_t* kbase, const uint16_t* vbase, int64_t
     p2[m] = pack_h2(p[2 * m], p[2 * m + 1]);
     psum = dot2(p2[m], kOnes2, psum);
   }
-  acc.l = acc.l * alpha + psum;
-  acc.m = m_new;
-#pragma unroll
-  for (int b = 0; b < NB; ++b) acc.o[b] *= alpha;
+  acc.l += psum;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     const uint32_t sel = sel_halves(b & 1);
@@ -593,15 +610,18 @@ __device__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_begin, in
     __builtin_amdgcn_wave_barrier();
     const int t_next = t0 + kTile * kWaves;
     if (t_next < t_end) load_group<HD, KB, VB>(regs, s, o, kfast, t_next, min(kTile, t_end - t_next), lane);
-    kivi_group<HD, KB, VB>(nvalid, lds_wave, qh, acc, sl2, lane);
+    if (nvalid == kTile) kivi_group<HD, KB, VB, true>(nvalid, lds_wave, qh, acc, sl2, lane);
+    else kivi_group<HD, KB, VB, false>(nvalid, lds_wave, qh, acc, sl2, lane);
     __builtin_amdgcn_wave_barrier();
     if (t_next >= t_end) break;
     t0 = t_next;
   }
 }
 
-template <int HD>
-__global__ void __launch_bounds__(256)
+// Two workgroups (8 waves) per CU: the register budget is capped so a second
+// wave per SIMD hides LDS and dependency latency.
+template <int HD, int MAXB>
+__global__ void __launch_bounds__(256, 2)
 decode_mfma_kernel(const DecodeParams p) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr int NB = HD / 16;
@@ -620,7 +640,10 @@ decode_mfma_kernel(const DecodeParams p) {
 
   int si = 0;
   while (si + 1 < p.nseg && (int)blockIdx.x >= p.seg[si + 1].lbegin) ++si;
-  const SegDev& s = p.seg[si];
+  // a register copy: fields read inside the group loop must not be reloaded
+  // from the argument block (such a reload would sit in the in-order memory
+  // counter behind the prefetched group and stall on it)
+  const SegDev s = p.seg[si];
   const int local = blockIdx.x - s.lbegin;
   const int cg = s.gbegin + local;
   int len_b = s.length;
@@ -629,15 +652,16 @@ decode_mfma_kernel(const DecodeParams p) {
   const int t_end = min(t_begin + s.chunk_len, len_b);
   const float sl2 = p.scale * kLog2e;
 
-  // q of head n (zero for padding heads): lane's channels 32 s + 8 g4 .. + 7
+  // q of head n, lane's channels 32 s + 8 g4 .. + 7.  Padding columns (n >= nh)
+  // repeat the slab's last head; their results are never written, and the
+  // loads stay unconditional so they do not serialize with the first group's.
   u4_t qb[KS];
   uint32_t qh[HD / 8];
+  const int nq = min(n, nh - 1);
 #pragma unroll
   for (int k = 0; k < KS; ++k) {
-    u4_t v = {0u, 0u, 0u, 0u};
-    if (n < nh)
-      v = *reinterpret_cast<const u4_t*>(p.q + (int64_t)b * p.q_bs + (int64_t)(h0 + n) * p.q_hs +
-                                         32 * k + 8 * g4);
+    const u4_t v = *reinterpret_cast<const u4_t*>(p.q + (int64_t)b * p.q_bs +
+                                                  (int64_t)(h0 + nq) * p.q_hs + 32 * k + 8 * g4);
     qb[k] = v;
 #pragma unroll
     for (int m = 0; m < 4; ++m) qh[4 * k + m] = v[m];
@@ -649,6 +673,7 @@ decode_mfma_kernel(const DecodeParams p) {
 #pragma unroll
   for (int i = 0; i < HD / 32; ++i) acc.vb[i] = 0.f;
   acc.m = -INFINITY;
+  acc.mx = -INFINITY;
   acc.l = 0.f;
 
   char* lds_wave = lds + wave * p.wave_lds;
@@ -663,15 +688,29 @@ decode_mfma_kernel(const DecodeParams p) {
     o.km = b * s.km_bs + kvh * s.km_hs;
     o.vd = b * s.vd_bs + kvh * s.vd_hs;
     o.vm = b * s.vm_bs + kvh * s.vm_hs;
-#define PK_KIVI_CASE(KB_, VB_)                                                               \
-  if (s.kbits == KB_ && s.vbits == VB_)                                                      \
-    kivi_chunk<HD, KB_, VB_>(s, o, t_begin, t_end, wave, lane, lds_wave, qh, acc, sl2);
-    PK_KIVI_CASE(2, 2) else PK_KIVI_CASE(2, 4) else PK_KIVI_CASE(2, 8)
-    else PK_KIVI_CASE(4, 2) else PK_KIVI_CASE(4, 4) else PK_KIVI_CASE(4, 8)
-    else PK_KIVI_CASE(8, 2) else PK_KIVI_CASE(8, 4) else PK_KIVI_CASE(8, 8)
+    // only the bit widths up to MAXB are compiled into this kernel variant,
+    // which keeps the register budget of the common 2/4-bit cases low
+#define PK_KIVI_CASE(KB_, VB_)                                                                 \
+  if constexpr (KB_ <= MAXB && VB_ <= MAXB) {                                                  \
+    if (s.kbits == KB_ && s.vbits == VB_)                                                      \
+      kivi_chunk<HD, KB_, VB_>(s, o, t_begin, t_end, wave, lane, lds_wave, qh, acc, sl2);      \
+  }
+    PK_KIVI_CASE(2, 2) PK_KIVI_CASE(2, 4) PK_KIVI_CASE(2, 8)
+    PK_KIVI_CASE(4, 2) PK_KIVI_CASE(4, 4) PK_KIVI_CASE(4, 8)
+    PK_KIVI_CASE(8, 2) PK_KIVI_CASE(8, 4) PK_KIVI_CASE(8, 8)
 #undef PK_KIVI_CASE
   }
 
+  // ---- report (m, l, acc) against the true max of the wave's scores ----
+  if (acc.mx != -INFINITY) {
+    const float alpha = __builtin_amdgcn_exp2f(acc.m - acc.mx);
+    acc.m = acc.mx;
+    acc.l *= alpha;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) acc.o[i] *= alpha;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) acc.vb[i] *= alpha;
+  }
   // ---- wave results -> LDS, merge the 4 waves ----
   __syncthreads();
   float* mo = reinterpret_cast<float*>(lds);               // [4][16][HD]
@@ -738,7 +777,7 @@ decode_mfma_kernel(const DecodeParams p) {
 
 // LDS bytes per wave for the largest K / V bit widths of a launch
 static int kivi_wave_bytes(int hd, int kb, int vb) {
-  return 4 * hd * (kb + vb + 2);
+  return 4 * (hd + 8) * kb + 4 * hd * (vb + 2);
 }
 
 int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, int max_vbits,
@@ -750,10 +789,15 @@ int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, in
   const size_t merge = sizeof(float) * ((size_t)kWaves * 16 * hd + 2 * kWaves * 16);
   const size_t lds = std::max(staging, merge);
   dim3 grid(lchunks, dp.Hkv * dp.nslab, dp.B);
-  if (hd == 128)
-    hipLaunchKernelGGL(decode_mfma_kernel<128>, grid, dim3(256), lds, stream, dp);
-  else
-    hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(256), lds, stream, dp);
+  const int maxb = std::max(max_kbits, max_vbits);
+#define PK_LAUNCH(HD_, MB_) \
+  hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_mfma_kernel<HD_, MB_>), grid, dim3(256), lds, stream, dp)
+  if (hd == 128) {
+    if (maxb <= 2) PK_LAUNCH(128, 2); else if (maxb <= 4) PK_LAUNCH(128, 4); else PK_LAUNCH(128, 8);
+  } else {
+    if (maxb <= 2) PK_LAUNCH(64, 2); else if (maxb <= 4) PK_LAUNCH(64, 4); else PK_LAUNCH(64, 8);
+  }
+#undef PK_LAUNCH
   return check_launch("decode_mfma");
 }
 
