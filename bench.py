@@ -1,7 +1,7 @@
 """Benchmark of the PhaseKV Stage-B decode attention on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-sweep] [--no-cpu]
-                    [--no-dense]
+                    [--no-dense] [--copy-probe-mib M]
 
 A step is one decode-attention call (one layer, one query token) over the
 packed prompt tier, the cold tier and the FP16 hot window of the workload.
@@ -10,6 +10,12 @@ a different copy of the tiers, and the copies together exceed twice the
 256 MB MALL, so the timed bytes come from HBM.  ``value`` is the achieved
 algorithmic HBM bandwidth (packed K/V codes + fp16 scale/min + fp16 hot
 window + q + output per step) divided by the measured step time.
+
+``roofline`` is the partials kernel (``pk::decode_mfma_kernel``, which reads
+every KV byte; the combine launch reads only the small workspace) timed on its
+own the same way: algorithmic bytes per launch / its average launch time, and
+``traffic``, the HBM bytes per launch that rocprofv3's FETCH_SIZE + WRITE_SIZE
+counters read for it, from the committed PMC summary.
 
 Prints ONE JSON line (rank 0).  Extra fields: ``us_per_step``, the FP16 dense
 GQA-aware comparator on the same tokens, and ``sweep``: the same measurement
@@ -63,9 +69,12 @@ def _time_graph(fns, steps: int, warmup: int, stream) -> float:
 
 
 def _bench_config(cfg, device, steps, warmup, stream, with_dense=True):
+    """Step time (partials + combine) and the partials kernel's own time on rotating copies."""
+    from phasekv_amd import decode as dec
     from phasekv_amd import workloads
-    from phasekv_amd.kernels.attention_triton import (dense_fp16_decode, fused_phasekv_decode,
-                                                      fused_phasekv_decode_batched)
+    from phasekv_amd.kernels.attention_triton import (fused_phasekv_decode,
+                                                      fused_phasekv_decode_batched,
+                                                      phasekv_problem)
     wl = workloads.make_workload(cfg, device, keep_dense=with_dense)
     nbytes = wl.bytes
     copies = _copies_for(nbytes)
@@ -73,17 +82,23 @@ def _bench_config(cfg, device, steps, warmup, stream, with_dense=True):
     q = wl.q
     if cfg.batch == 1:
         fns = [lambda t=t: fused_phasekv_decode(q[0], t, cfg.hq) for t in tiers]
+        probs = [phasekv_problem(q[0], t, cfg.hq) for t in tiers]
     else:
         fns = [lambda t=t: fused_phasekv_decode_batched(q, t, cfg.hq, wl.prompt_lens) for t in tiers]
+        probs = [phasekv_problem(q, t, cfg.hq, batched=True, prompt_lens=wl.prompt_lens)
+                 for t in tiers]
     sec = _time_graph(fns, steps, warmup, stream)
+    # the dominant kernel alone: the same steps without the combine launch
+    ksec = _time_graph([lambda pr=pr: dec.launch_partials(pr) for pr in probs], steps, warmup,
+                       stream)
     res = {"config": cfg.name, "tokens": cfg.tokens, "bytes": nbytes, "copies": copies,
-           "us_per_step": sec * 1e6, "gbs": nbytes / sec / 1e9}
+           "us_per_step": sec * 1e6, "gbs": nbytes / sec / 1e9,
+           "partials_us": ksec * 1e6, "partials_gbs": nbytes / ksec / 1e9}
     res["frac"] = res["gbs"] / HBM_PEAK_GBS
-    del tiers, fns
+    del tiers, fns, probs
     if with_dense:
         # uncompressed fp16 K/V of the same tokens (prompt rows at their ragged lengths),
         # read by the same GQA-aware kernel as the hot window: no expanded copies
-        from phasekv_amd import decode as dec
         dense = [(k.to(device), v.to(device)) for k, v in zip(wl.dense_k, wl.dense_v)
                  if k is not None]
         dbytes = workloads.fp16_dense_bytes(cfg, wl.prompt_lens_list if cfg.ragged_min else None)
@@ -139,6 +154,40 @@ def _cpu_baseline(cfg_name: str, budget_s: float = 10.0):
                       "(dequantize every tier, concat, GQA expand, fp32 softmax attention), median"}
 
 
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "decode_mfma_traffic.md")
+
+
+def _measured_traffic(cfg_name: str):
+    """HBM bytes per partials launch from the committed rocprofv3 PMC summary, if any.
+
+    The summary holds lines ``traffic_bytes_per_launch <config> <bytes>``: FETCH_SIZE +
+    WRITE_SIZE per dispatch of the partials kernel, each scaled by what the same counter
+    reads for a copy of known size.
+    """
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            for line in fh:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == cfg_name:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
+def _copy_probe(mib: int, device) -> None:
+    """Three plain device copies of ``mib`` MiB: the calibration dispatches of a PMC run."""
+    src = torch.ones(mib << 19, dtype=torch.float16, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    _log(f"bench: copy probe {mib} MiB read + {mib} MiB written per dispatch, 3 dispatches")
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,6 +198,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-dense", action="store_true", help="skip the FP16 dense comparator")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run plain copies of this size (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the decode path "
@@ -162,6 +213,8 @@ def main() -> int:
     device = torch.device("cuda:0")
     stream = torch.cuda.Stream(device)
     cfg = workloads.CONFIGS[args.config]
+    if args.copy_probe_mib > 0:
+        _copy_probe(args.copy_probe_mib, device)
     _log(f"bench: {cfg} steps={args.steps} warmup={args.warmup}")
     main_res, _ = _bench_config(cfg, device, args.steps, args.warmup, stream,
                                 with_dense=not args.no_dense)
@@ -189,15 +242,18 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 accumulate (2/4-bit packed KV, fp16 q and hot window)",
+        "dtype": "f16",
         "data": "synthetic: seeded N(0,1) K/V with 4 outlier K channels per kv head x8",
         "config": {"workload": f"{cfg.name}: Qwen2.5-7B decode attention, Hq{cfg.hq}/Hkv{cfg.hkv}/"
                                f"hd{cfg.hd}, prompt {cfg.prompt}@{cfg.prompt_bits}b, cold "
                                f"{cfg.cold}@{cfg.cold_bits}b, hot {cfg.hot} fp16, batch {cfg.batch}",
                    "global_batch": cfg.batch, "seq_len": cfg.tokens, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(main_res["gbs"], 3), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(main_res["frac"], 5), "traffic": None,
-                     "bytes_per_launch": main_res["bytes"]},
+        "roofline": {"bound": "hbm", "kernel": "pk::decode_mfma_kernel",
+                     "achieved": round(main_res["partials_gbs"], 3), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(main_res["partials_gbs"] / HBM_PEAK_GBS, 5),
+                     "traffic": _measured_traffic(cfg.name),
+                     "bytes_per_launch": main_res["bytes"],
+                     "launch_us": round(main_res["partials_us"], 3)},
         "cpu_baseline": cpu,
         "us_per_step": round(main_res["us_per_step"], 3),
         "fp16_dense_us": round(main_res.get("fp16_dense_us", float("nan")), 3),

@@ -8,7 +8,8 @@ namespace pk {
 constexpr int kThreads = 256;                 // threads per decode workgroup
 constexpr int kMaxSeg = PK_MAX_SEGMENTS_PER_LAUNCH;
 constexpr int kCombineMaxHd = 256;            // largest head_dim handled by the combine
-constexpr int kCombineRegs = 32;             // partial loads in flight per combine thread
+constexpr int kCombineLoads = 8;             // partials in flight per combine thread
+constexpr int kCombineTarget = 4;            // partials per combine thread the host aims at
 constexpr int kMinChunk = 64;                 // auto chunk lengths are multiples of this
 
 // One segment as the kernels see it (element strides, see pk_segment).

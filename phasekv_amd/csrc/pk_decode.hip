@@ -192,88 +192,90 @@ decode_partials_generic(const DecodeParams p) {
   }
 }
 
-// Log-sum-exp merge of the C partials of one output row per workgroup
-// (attention_triton.py:257-266, 300-307).  Thread (cs, d) owns channel d of
-// partials cs, cs + ncs, ...: it issues all of its loads (up to kCombineRegs
-// per pass) before using any, together with the row's m / l, so a pass costs
-// one memory round trip; the weights exp(m_c - M) go through LDS and the
-// channel sums of the ncs slices are added through LDS.
+// Log-sum-exp merge of the C partials of each output row
+// (attention_triton.py:257-266, 300-307).  A workgroup owns one row and a slice
+// of hs channels (16 <= hs <= 64, chosen by the host from C: many partials per
+// row give narrow slices, so a batch-1 decode still spreads over rows * hd / 16
+// workgroups).  Thread (cs, d) owns channel d of partials cs, cs + ncs, ...
+// (ncs = 256 / hs): it loads m, l and acc of up to kCombineLoads of them at
+// once, so a pass is one memory round trip.  The
+// row maximum is a wave shuffle reduction plus one LDS exchange between the
+// four waves; the sums over cs are the same, once, at the end.
+__device__ inline float wave_max_over(float v, int from) {
+  for (int o = from; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ inline float wave_sum_over(float v, int from) {
+  for (int o = from; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 __global__ void __launch_bounds__(kThreads)
 combine_kernel(const float* __restrict__ m, const float* __restrict__ l,
-               const float* __restrict__ acc, int C, int hd, uint16_t* out, float* om, float* ol,
-               float* oacc) {
-  extern __shared__ float cw[];             // [C] weights
-  __shared__ float red[kThreads];
-  const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
+               const float* __restrict__ acc, int C, int hd, int hs, uint16_t* out, float* om,
+               float* ol, float* oacc) {
+  __shared__ float xch[kThreads / 64][65];   // [wave][channel], [wave][64] = l
+  const int tid = threadIdx.x, wave = tid / 64;
+  const int nsl = hd / hs;
+  const int64_t row = blockIdx.x / nsl;
+  const int d = (blockIdx.x % nsl) * hs + tid % hs;
+  const int ncs = kThreads / hs, cs = tid / hs;
   const float* mr = m + row * C;
   const float* lr = l + row * C;
-  const float* ar = acc + row * (int64_t)C * hd;
-  const int ncs = kThreads / hd;            // hd <= 256, a power of two
-  const int d = tid % hd, cs = tid / hd;
-  float sum = 0.f, ls = 0.f;
-  float M = -INFINITY;
-  for (int base = 0; base < C; base += kCombineRegs * ncs) {
-    // ---- issue every load of this pass ----
-    float a[kCombineRegs];
+  const float* ar = acc + row * (int64_t)C * hd + d;
+  float M = -INFINITY, sum = 0.f, ls = 0.f;
+  for (int base = 0; base < C; base += kCombineLoads * ncs) {
+    float a[kCombineLoads], mk[kCombineLoads], lk[kCombineLoads];
 #pragma unroll
-    for (int k = 0; k < kCombineRegs; ++k) {
+    for (int k = 0; k < kCombineLoads; ++k) {
       const int c = base + cs + k * ncs;
-      a[k] = (c < C) ? ar[(int64_t)c * hd + d] : 0.f;
+      const bool ok = c < C;
+      a[k] = ok ? ar[(int64_t)c * hd] : 0.f;
+      mk[k] = ok ? mr[c] : -INFINITY;
+      lk[k] = ok ? lr[c] : 0.f;
     }
-    float mloc = -INFINITY;
-    float lloc = 0.f;
-    for (int c = base + tid; c < min(C, base + kCombineRegs * ncs); c += kThreads) {
-      const float mc = mr[c];
-      cw[c - base] = mc;
-      mloc = fmaxf(mloc, mc);
-    }
-    // ---- running max over the passes so far ----
-    red[tid] = mloc;
-    __syncthreads();
-    for (int st = kThreads / 2; st > 0; st >>= 1) {
-      if (tid < st) red[tid] = fmaxf(red[tid], red[tid + st]);
-      __syncthreads();
-    }
-    const float Mn = fmaxf(M, red[0]);
-    const float scale_old = (M == -INFINITY) ? 0.f : expf(M - Mn);
-    M = Mn;
-    __syncthreads();
-    for (int c = base + tid; c < min(C, base + kCombineRegs * ncs); c += kThreads) {
-      const float mc = cw[c - base];
-      const float w = (mc == -INFINITY) ? 0.f : expf(mc - M);
-      cw[c - base] = w;
-      lloc += w * lr[c];
-    }
-    __syncthreads();
-    float part = 0.f;
+    float mx = mk[0];
 #pragma unroll
-    for (int k = 0; k < kCombineRegs; ++k) {
-      const int c = base + cs + k * ncs;
-      if (c < C) part += cw[c - base] * a[k];
+    for (int k = 1; k < kCombineLoads; ++k) mx = fmaxf(mx, mk[k]);
+    mx = wave_max_over(mx, hs);
+    if ((tid & 63) == 0) xch[wave][0] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) mx = fmaxf(mx, xch[w][0]);
+    __syncthreads();
+    const float Mn = fmaxf(M, mx);
+    if (Mn != -INFINITY) {
+      const float so = (M == -INFINITY) ? 0.f : expf(M - Mn);
+      sum *= so;
+      ls *= so;
+#pragma unroll
+      for (int k = 0; k < kCombineLoads; ++k) {
+        const float w = (mk[k] == -INFINITY) ? 0.f : expf(mk[k] - Mn);
+        sum += w * a[k];
+        ls += w * lk[k];
+      }
+      M = Mn;
     }
-    sum = sum * scale_old + part;
-    ls = ls * scale_old + lloc;
-    __syncthreads();
   }
-  red[tid] = ls;
+  // every lane of one cs holds the same ls: sum over cs lanes, then over waves
+  sum = wave_sum_over(sum, hs);
+  ls = wave_sum_over(ls, hs);
+  if ((tid & 63) < hs) xch[wave][tid & 63] = sum;
+  if ((tid & 63) == 0) xch[wave][64] = ls;
   __syncthreads();
-  for (int st = kThreads / 2; st > 0; st >>= 1) {
-    if (tid < st) red[tid] += red[tid + st];
-    __syncthreads();
-  }
-  const float L = red[0];
-  __syncthreads();
-  red[tid] = sum;
-  __syncthreads();
-  if (cs == 0) {
-    for (int k = 1; k < ncs; ++k) sum += red[k * hd + d];
-    if (out) out[row * hd + d] = pk_f2h(sum / L);
-    if (oacc) oacc[row * hd + d] = sum;
-  }
-  if (om && tid == 0) {
-    om[row] = M;
-    ol[row] = L;
+  if (tid < hs) {
+    float S = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+      S += xch[w][tid];
+      L += xch[w][64];
+    }
+    if (out) out[row * hd + d] = pk_f2h(S / L);
+    if (oacc) oacc[row * hd + d] = S;
+    if (om && d == 0) {
+      om[row] = M;
+      ol[row] = L;
+    }
   }
 }
 
@@ -535,9 +537,14 @@ static int launch_combine(const float* m, const float* l, const float* acc, int6
                           int hd, uint16_t* out, float* om, float* ol, float* oacc,
                           hipStream_t stream, const char* what) {
   if (rows == 0) return PK_OK;
-  const size_t lds = sizeof(float) * (size_t)std::min(C, kCombineRegs * kThreads);
-  hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(kThreads), lds, stream, m, l, acc, C, hd,
-                     out, om, ol, oacc);
+  // about kCombineTarget partials per thread, at least 4 and at most 16 partial lanes
+  int ncs = 4;
+  while (ncs < 16 && ncs * kCombineTarget < C) ncs <<= 1;
+  const int hs = std::min(hd, kThreads / ncs);
+  const int64_t blocks = rows * (hd / hs);
+  if (blocks > INT32_MAX) return fail("too many output rows");
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, m, l, acc,
+                     C, hd, hs, out, om, ol, oacc);
   return check_launch(what);
 }
 

@@ -207,6 +207,14 @@ def fused_decode(problem: Problem) -> torch.Tensor:
     return out
 
 
+def launch_partials(problem: Problem) -> None:
+    """Only the split-partials launch, into the cached workspace (for timing the kernel)."""
+    nbytes, _ = problem.workspace_size()
+    ws = cached_workspace(problem.device, nbytes)
+    _lib.check(_lib.load().pk_decode_partials(ctypes.byref(problem.c), ws.data_ptr(), ws.numel(),
+                                              _lib.stream_ptr(problem.device)), "decode_partials")
+
+
 def decode_partials(problem: Problem):
     """Raw split partials: (pm [B*Hq, C], pl [B*Hq, C], pacc [B*Hq, C, hd]) in a fresh buffer."""
     nbytes, splits = problem.workspace_size()

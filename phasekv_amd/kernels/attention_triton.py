@@ -8,10 +8,9 @@ hand-written HIP kernels of ``libphasekv_hip.so`` through its C ABI.
 Differences in *how*, not *what*:
 
 * ``fused_phasekv_decode`` covers the prompt segment, every prompt extension,
-  every cold segment and the FP16 hot window in ONE launch (per 8 segments):
-  split partials are merged by the last workgroup of each kv head, instead of
-  one Triton launch per segment plus ~25 torch ops
-  (``attention_triton.py:643-669``).
+  every cold segment and the FP16 hot window in ONE partials launch (per 8
+  segments) plus ONE log-sum-exp combine launch, instead of one Triton launch
+  per segment plus ~25 torch ops (``attention_triton.py:643-669``).
 * One workgroup serves all query heads of a GQA group, so each packed K/V byte
   is read once per kv head, not once per query head (``attention_triton.py:534``).
 * ``num_splits`` / ``block_n`` / ``num_warps`` are validated exactly as the
@@ -208,17 +207,17 @@ def _remove_batch(pt: PackedTensor) -> PackedTensor:
                    orig_shape=tuple(pt.orig_shape[1:]), axis=pt.axis - 1)
 
 
-def fused_phasekv_decode(q: torch.Tensor, tiers, num_attention_heads: int,
-                         num_splits: int | None = None, block_n: int | None = None,
-                         num_warps: int | None = None) -> torch.Tensor:
-    """batch=1 PhaseKV decode attention over every packed segment and the hot window.
-
-    ``tiers`` is ``PhaseKVCache.layer_tiers(i)`` (or any object with ``prompt``,
-    ``prompt_extensions``, ``cold``, ``hot_len`` and ``hot_views()``).  q ``[Hq, hd]``
-    fp16 -> ``[Hq, hd]`` fp16 (``attention_triton.py:643-669``).
-    """
+def phasekv_problem(q: torch.Tensor, tiers, num_attention_heads: int, batched: bool = False,
+                    prompt_lens: torch.Tensor | None = None, num_splits: int | None = None,
+                    block_n: int | None = None, num_warps: int | None = None) -> _dec.Problem:
+    """The decode problem (every packed segment + the hot window) of one layer's tiers."""
     segs = []
-    for segment in [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]:
+    for i, segment in enumerate([tiers.prompt, *tiers.prompt_extensions, *tiers.cold]):
+        if batched:
+            lens = prompt_lens.to(torch.int32) if (i == 0 and prompt_lens is not None) else None
+            segs.append(_dec.packed_segment(segment.key, segment.value, batched=True,
+                                            seq_lens=lens))
+            continue
         key, value = _remove_batch(segment.key), _remove_batch(segment.value)
         if key.axis != 1 or value.axis != 2:
             raise ValueError("K must be packed along tokens and V along head_dim")
@@ -229,8 +228,23 @@ def fused_phasekv_decode(q: torch.Tensor, tiers, num_attention_heads: int,
                                         split_len=split_len))
     if tiers.hot_len:
         hot_k, hot_v = tiers.hot_views()
-        segs.append(_dec.fp16_segment(hot_k[0], hot_v[0], batched=False))
-    return _dec.fused_decode(_dec.Problem(q, segs, num_attention_heads))[0]
+        segs.append(_dec.fp16_segment(hot_k if batched else hot_k[0],
+                                      hot_v if batched else hot_v[0], batched=batched))
+    return _dec.Problem(q, segs, num_attention_heads)
+
+
+def fused_phasekv_decode(q: torch.Tensor, tiers, num_attention_heads: int,
+                         num_splits: int | None = None, block_n: int | None = None,
+                         num_warps: int | None = None) -> torch.Tensor:
+    """batch=1 PhaseKV decode attention over every packed segment and the hot window.
+
+    ``tiers`` is ``PhaseKVCache.layer_tiers(i)`` (or any object with ``prompt``,
+    ``prompt_extensions``, ``cold``, ``hot_len`` and ``hot_views()``).  q ``[Hq, hd]``
+    fp16 -> ``[Hq, hd]`` fp16 (``attention_triton.py:643-669``).
+    """
+    problem = phasekv_problem(q, tiers, num_attention_heads, num_splits=num_splits,
+                              block_n=block_n, num_warps=num_warps)
+    return _dec.fused_decode(problem)[0]
 
 
 def fused_phasekv_decode_batched(q: torch.Tensor, tiers, num_attention_heads: int,
@@ -242,14 +256,8 @@ def fused_phasekv_decode_batched(q: torch.Tensor, tiers, num_attention_heads: in
     token 0) and padded to the tier's length.  Beyond the reference, which
     takes batch = 1 only.
     """
-    segs = []
-    for i, segment in enumerate([tiers.prompt, *tiers.prompt_extensions, *tiers.cold]):
-        lens = prompt_lens.to(torch.int32) if (i == 0 and prompt_lens is not None) else None
-        segs.append(_dec.packed_segment(segment.key, segment.value, batched=True, seq_lens=lens))
-    if tiers.hot_len:
-        hot_k, hot_v = tiers.hot_views()
-        segs.append(_dec.fp16_segment(hot_k, hot_v, batched=True))
-    return _dec.fused_decode(_dec.Problem(q, segs, num_attention_heads))
+    return _dec.fused_decode(phasekv_problem(q, tiers, num_attention_heads, batched=True,
+                                             prompt_lens=prompt_lens))
 
 
 def dense_fp16_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
