@@ -12,6 +12,31 @@ constexpr int kCombineLoads = 8;             // partials in flight per combine t
 constexpr int kCombineTarget = 4;            // partials per combine thread the host aims at
 constexpr int kMinChunk = 64;                 // auto chunk lengths are multiples of this
 
+constexpr uint32_t kXcds = 8;                 // accelerator complex dies of an MI355X
+
+// The workgroup's coordinates in an XCD-contiguous order.  The dispatcher hands
+// consecutive workgroups (x fastest, then y, then z) round-robin to the 8 XCDs,
+// each with its own L2.  Renumbering the linear id so that XCD i runs the i-th
+// contiguous eighth of the grid makes neighbouring chunks of one kv row, which
+// share the cache lines of the token-packed K codes and of the K scales, meet
+// in one L2 instead of being fetched once per XCD.
+struct Block3 {
+  int x, y, z;
+};
+__device__ inline Block3 xcd_block() {
+  const uint32_t gx = gridDim.x, gy = gridDim.y;
+  const uint32_t n = gx * gy * gridDim.z;
+  const uint32_t lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const uint32_t xcd = lin % kXcds, k = lin / kXcds;
+  const uint32_t q = n / kXcds, r = n % kXcds;
+  const uint32_t id = xcd * q + (xcd < r ? xcd : r) + k;
+  Block3 o;
+  o.x = (int)(id % gx);
+  o.y = (int)((id / gx) % gy);
+  o.z = (int)(id / (gx * gy));
+  return o;
+}
+
 // One segment as the kernels see it (element strides, see pk_segment).
 struct SegDev {
   int kind, length, kbits, vbits, kgs, vgs;

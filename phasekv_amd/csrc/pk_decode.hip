@@ -71,16 +71,17 @@ decode_partials_generic(const DecodeParams p) {
   float* l_s = m_s + HS;                  // [HS]
   float* a_s = l_s + HS;                  // [HS]
 
-  const int b = blockIdx.z;
-  const int kvh = blockIdx.y / p.nslab;
-  const int slab = blockIdx.y - kvh * p.nslab;
+  const Block3 blk = xcd_block();
+  const int b = blk.z;
+  const int kvh = blk.y / p.nslab;
+  const int slab = blk.y - kvh * p.nslab;
   const int h0 = kvh * p.G + slab * HS;
   const int nh = min(HS, p.G - slab * HS);
 
   int si = 0;
-  while (si + 1 < p.nseg && (int)blockIdx.x >= p.seg[si + 1].lbegin) ++si;
+  while (si + 1 < p.nseg && blk.x >= p.seg[si + 1].lbegin) ++si;
   const SegDev& s = p.seg[si];
-  const int local = blockIdx.x - s.lbegin;
+  const int local = blk.x - s.lbegin;
   const int cg = s.gbegin + local;
   int len_b = s.length;
   if (s.seq_lens) len_b = min(len_b, s.seq_lens[b]);
@@ -217,8 +218,9 @@ combine_kernel(const float* __restrict__ m, const float* __restrict__ l,
   __shared__ float xch[kThreads / 64][65];   // [wave][channel], [wave][64] = l
   const int tid = threadIdx.x, wave = tid / 64;
   const int nsl = hd / hs;
-  const int64_t row = blockIdx.x / nsl;
-  const int d = (blockIdx.x % nsl) * hs + tid % hs;
+  const int wg = xcd_block().x;               // slices of one row share cache lines
+  const int64_t row = wg / nsl;
+  const int d = (wg % nsl) * hs + tid % hs;
   const int ncs = kThreads / hs, cs = tid / hs;
   const float* mr = m + row * C;
   const float* lr = l + row * C;

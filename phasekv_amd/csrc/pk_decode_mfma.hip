@@ -632,19 +632,20 @@ decode_mfma_kernel(const DecodeParams p) {
   const int n = lane & 15;
   const int g4 = lane >> 4;
 
-  const int b = blockIdx.z;
-  const int kvh = blockIdx.y / p.nslab;
-  const int slab = blockIdx.y - kvh * p.nslab;
+  const Block3 blk = xcd_block();
+  const int b = blk.z;
+  const int kvh = blk.y / p.nslab;
+  const int slab = blk.y - kvh * p.nslab;
   const int h0 = kvh * p.G + slab * p.HS;
   const int nh = min(p.HS, p.G - slab * p.HS);
 
   int si = 0;
-  while (si + 1 < p.nseg && (int)blockIdx.x >= p.seg[si + 1].lbegin) ++si;
+  while (si + 1 < p.nseg && blk.x >= p.seg[si + 1].lbegin) ++si;
   // a register copy: fields read inside the group loop must not be reloaded
   // from the argument block (such a reload would sit in the in-order memory
   // counter behind the prefetched group and stall on it)
   const SegDev s = p.seg[si];
-  const int local = blockIdx.x - s.lbegin;
+  const int local = blk.x - s.lbegin;
   const int cg = s.gbegin + local;
   int len_b = s.length;
   if (s.seq_lens) len_b = min(len_b, s.seq_lens[b]);
