@@ -154,19 +154,18 @@ def _cpu_baseline(cfg_name: str, budget_s: float = 10.0):
                       "(dequantize every tier, concat, GQA expand, fp32 softmax attention), median"}
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "decode_mfma_traffic.md")
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 
 def _measured_traffic(cfg_name: str):
     """HBM bytes per partials launch from the committed rocprofv3 PMC summary, if any.
 
-    The summary holds lines ``traffic_bytes_per_launch <config> <bytes>``: FETCH_SIZE +
-    WRITE_SIZE per dispatch of the partials kernel, each scaled by what the same counter
-    reads for a copy of known size.
+    ``profiles/decode_mfma_<config>.md`` holds a line ``traffic_bytes_per_launch <config>
+    <bytes>``: FETCH_SIZE + WRITE_SIZE per dispatch of the partials kernel, each scaled by
+    what the same counter reads for a copy of known size (``--copy-probe-mib``).
     """
     try:
-        with open(TRAFFIC_PROFILE) as fh:
+        with open(os.path.join(PROFILES, f"decode_mfma_{cfg_name}.md")) as fh:
             for line in fh:
                 parts = line.split()
                 if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == cfg_name:
