@@ -64,7 +64,7 @@ struct DecodeParams {
   float* ws_acc;      // [B*Hq][C][hd]
   int C;              // chunks per (batch, kv head) over all segments
   int nseg;
-  int wave_lds;       // MFMA kernel: LDS bytes of one wave's tile staging
+  int stage_lds;      // MFMA kernel: LDS bytes of one stage buffer (two are used)
   SegDev seg[kMaxSeg];
 };
 

@@ -359,12 +359,16 @@ static bool mfma_eligible(const pk_decode_problem* p) {
       continue;
     }
     if (s.kind != PK_SEG_KIVI) return false;
-    if (!(s.k_group == 32 || s.k_group >= s.length) || s.v_group != 32) return false;
-    const int64_t row_bytes = ((int64_t)s.length * s.k_bits + 7) / 8;
-    const int64_t kcb = (s.k_bits == 2) ? 8 : 16;   // K load width of the kernel
-    const int64_t ra = (row_bytes % kcb == 0) ? kcb : (row_bytes % 4 == 0) ? 4 : 1;
-    if (!aligned(s.k_data, ra) || s.k_data_bstride % ra || s.k_data_hstride % ra) return false;
+    // K groups of 32 tokens, or one group for a segment of at most 32 tokens
+    if (!(s.k_group == 32 || (s.length <= 32 && s.k_group >= s.length)) || s.v_group != 32)
+      return false;
+    // K rows and K metadata are read at whatever alignment they have; V rows in
+    // 16-byte pieces and V metadata one token (hd / 32 fp16) per load
     if (!aligned(s.v_data, 16) || s.v_data_bstride % 16 || s.v_data_hstride % 16) return false;
+    const int vma = hd / 32;
+    if (!aligned(s.v_scale, 2 * vma) || !aligned(s.v_mins, 2 * vma) || s.v_meta_bstride % vma ||
+        s.v_meta_hstride % vma)
+      return false;
   }
   return true;
 }

@@ -139,155 +139,159 @@ __device__ __forceinline__ float lazy_rescale(WaveAcc<HD>& acc, float mt) {
 }
 
 // ---------------------------------------------------------------------------
-// per-wave LDS staging of one 32-token KIVI group
-//   Kw  uint32 [KB][HD + 8]     the group's K bytes of every channel row (rows padded
-//                               by 8 words so neighbouring words land in other banks)
-//   Ks, Km  fp16 [HD]           K scale / min of the group
-//   Vw  uint32 [32][HD*VB/32]   the group's V rows
-//   Vs, Vm  fp16 [HD/32][32]    V scale / min, channel group major
+// LDS staging of a 128-token stage: four 32-token groups, one per wave.  The
+// workgroup loads a stage together, in 16-byte pieces where the rows allow,
+// because the token-packed K codes and the per-channel K scales put every
+// channel in its own cache line: one wide request per channel and stage costs
+// far fewer L1 -> L2 requests than one narrow request per channel and group.
+// The store to LDS transposes what the matrix operands need transposed:
+//   Kw  uint32 [4 KB][HD + 16/KB]  word w of every channel's K codes; the row
+//                                  padding puts the KB pieces a wave stores
+//                                  at once in distinct banks
+//   Ks, Km  fp16 [4][HD]           K scale / min of the stage's groups
+//   Vw  [128][HD*VB/8]             the stage's V rows as stored
+//   Vs, Vm  fp16 [HD/32][128]      V scale / min, channel group major
 // ---------------------------------------------------------------------------
+constexpr int kStage = 128;
+
 template <int HD, int KB, int VB>
-struct KiviLayout {
-  static constexpr int kw_row = HD + 8;                   // words per Kw row
-  static constexpr int kw_bytes = KB * kw_row * 4;
+struct StageLayout {
+  static constexpr int kw_row = HD + 16 / KB;             // words per Kw row
+  static constexpr int kw_bytes = 4 * KB * kw_row * 4;
+  static constexpr int off_ks = kw_bytes;
+  static constexpr int off_km = off_ks + 4 * HD * 2;
+  static constexpr int off_vw = off_km + 4 * HD * 2;
   static constexpr int vrow_words = HD * VB / 32;
   static constexpr int vrow_bytes = HD * VB / 8;
-  static constexpr int vw_bytes = kTile * vrow_bytes;
-  static constexpr int off_ks = kw_bytes;
-  static constexpr int off_km = off_ks + 2 * HD;
-  static constexpr int off_vw = off_km + 2 * HD;
-  static constexpr int off_vs = off_vw + vw_bytes;
-  static constexpr int off_vm = off_vs + 2 * HD;
-  static constexpr int bytes = off_vm + 2 * HD;
+  static constexpr int off_vs = off_vw + kStage * vrow_bytes;
+  static constexpr int off_vm = off_vs + (HD / 32) * kStage * 2;
+  static constexpr int bytes = off_vm + (HD / 32) * kStage * 2;
 };
 
-// Registers of one group's global loads.  Every address is clamped into the
-// segment, so the loads are unconditional and a whole group's loads are
-// in flight together; K bytes of tokens past the end give scores that are
-// masked, and V rows / metadata of such tokens are multiplied by p = 0.
+// One lane's share of a stage's global loads (256 lanes).
 template <int HD, int KB, int VB>
-struct GroupRegs {
-  static constexpr int KCB = (KB == 2) ? 8 : 16;          // bytes per K load
-  static constexpr int KCR = 4 * KB / KCB;                // K loads per channel row
-  static constexpr int NK = HD * KCR / 64;                // K loads per lane
-  static constexpr int VCH = HD * VB / 4;                 // 16-byte V chunks per group
-  static constexpr int NV = (VCH + 63) / 64;              // V loads per lane
-  static constexpr int NKM = HD / 64;                     // K scale / min per lane
+struct StageRegs {
+  static constexpr int KP = HD * KB;                      // 16-byte K pieces (KB per channel)
+  static constexpr int NK = (KP + kThreads - 1) / kThreads;
+  static constexpr int VP = HD * VB;                      // 16-byte V pieces (the stage's rows)
+  static constexpr int NV = (VP + kThreads - 1) / kThreads;
   u4_t k[NK];
   u4_t v[NV];
-  uint16_t ks[NKM], km[NKM];
-  uint32_t vmeta[HD / 64];   // lane < 32: V scales of token lane, else V mins of token lane-32
+  u2_t km;     // lanes < 2 HD: the 4 group scales (lane < HD) or mins of channel lane % HD
+  u2_t vm;     // V scales (lanes < 128) or mins of token lane % 128 (HD = 64: low word only)
 };
 
 struct SegOffsets {
   int64_t kd, km, vd, vm;
 };
 
+// How a segment's K rows can be read: 16-byte pieces, dwords or bytes.
+struct KivLoad {
+  int64_t row_bytes;   // bytes of one channel's K codes
+  int row_groups;      // K groups per channel
+  int kmode;           // 16, 4 or 1
+  bool kmeta4;         // the 4 group scales of a stage are one aligned 8-byte load
+};
+
+// Loads of the stage starting at token ts (ts - segment start is a multiple of
+// 32).  Addresses stay inside the segment: K pieces past a row's end are not
+// loaded (their codes only feed masked scores), V rows and metadata are
+// clamped to the last valid token t_last, K metadata to the last group.
 template <int HD, int KB, int VB>
-__device__ __forceinline__ void load_group(GroupRegs<HD, KB, VB>& r, const SegDev& s,
-                                           const SegOffsets& o, bool kfast, int t0, int nvalid,
-                                           int lane) {
-  using R = GroupRegs<HD, KB, VB>;
-  if (kfast) {
-    const int64_t row_bytes = ((int64_t)s.length * KB + 7) / 8;
-    const int64_t byte0 = (int64_t)t0 * KB / 8;
+__device__ __forceinline__ void load_stage(StageRegs<HD, KB, VB>& r, const SegDev& s,
+                                           const SegOffsets& o, const KivLoad& kl, int ts,
+                                           int t_last, int tid) {
+  using R = StageRegs<HD, KB, VB>;
+  using L = StageLayout<HD, KB, VB>;
+  const int64_t byte0 = (int64_t)ts * KB / 8;
+  const uint8_t* krows = s.kd + o.kd;
 #pragma unroll
-    for (int i = 0; i < R::NK; ++i) {
-      const int q = lane + 64 * i;
-      const int c = q / R::KCR, u = q - c * R::KCR;
-      int64_t off = byte0 + R::KCB * u;
-      off = off < row_bytes ? off : row_bytes - R::KCB;
-      const uint8_t* src = s.kd + o.kd + c * row_bytes + off;
-      if (KB == 2) {
-        const u2_t x = *reinterpret_cast<const u2_t*>(src);
-        r.k[i] = u4_t{x[0], x[1], 0u, 0u};
+  for (int i = 0; i < R::NK; ++i) {
+    const int q = tid + kThreads * i;
+    if (R::KP % kThreads == 0 || q < R::KP) {
+      const int c = q / KB, j = q - c * KB;
+      const int64_t off = byte0 + 16 * j;
+      const uint8_t* src = krows + c * kl.row_bytes + off;
+      u4_t v = {0u, 0u, 0u, 0u};
+      if (kl.kmode == 16) {
+        if (off < kl.row_bytes) v = *reinterpret_cast<const u4_t*>(src);
+      } else if (kl.kmode == 4) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          if (off + 4 * w < kl.row_bytes) v[w] = *reinterpret_cast<const uint32_t*>(src + 4 * w);
       } else {
-        r.k[i] = *reinterpret_cast<const u4_t*>(src);
+#pragma unroll
+        for (int bt = 0; bt < 16; ++bt)
+          if (off + bt < kl.row_bytes) v[bt >> 2] |= (uint32_t)src[bt] << (8 * (bt & 3));
       }
+      r.k[i] = v;
     }
   }
-  const int row_groups = (s.length + s.kgs - 1) / s.kgs;
-  const int g = t0 / 32;
+  if (tid < 2 * HD) {
+    const int c = tid % HD;
+    const uint16_t* m = ((tid < HD) ? s.ks : s.km) + o.km + (int64_t)c * kl.row_groups;
+    const int g0 = min(ts / 32, kl.row_groups - 1);
+    if (kl.kmeta4) {
+      r.km = *reinterpret_cast<const u2_t*>(m + g0);
+    } else {
+      uint32_t x[4];
 #pragma unroll
-  for (int i = 0; i < R::NKM; ++i) {
-    const int c = lane + 64 * i;
-    r.ks[i] = s.ks[o.km + (int64_t)c * row_groups + g];
-    r.km[i] = s.km[o.km + (int64_t)c * row_groups + g];
+      for (int g = 0; g < 4; ++g) x[g] = m[min(g0 + g, kl.row_groups - 1)];
+      r.km = u2_t{x[0] | (x[1] << 16), x[2] | (x[3] << 16)};
+    }
   }
-  const int last_chunk = nvalid * R::VCH / kTile - 1;   // last 16-byte chunk of a valid row
-  const uint8_t* vsrc = s.vd + o.vd + (int64_t)t0 * (HD * VB / 8);
+  const int last_piece = (t_last - ts + 1) * (L::vrow_bytes / 16) - 1;
+  const uint8_t* vsrc = s.vd + o.vd + (int64_t)ts * L::vrow_bytes;
 #pragma unroll
   for (int i = 0; i < R::NV; ++i) {
-    int q = lane + 64 * i;
-    q = q < last_chunk ? q : last_chunk;
-    r.v[i] = *reinterpret_cast<const u4_t*>(vsrc + (int64_t)q * 16);
+    const int q = tid + kThreads * i;
+    if (R::VP % kThreads == 0 || q < R::VP)
+      r.v[i] = *reinterpret_cast<const u4_t*>(vsrc + (int64_t)min(q, last_piece) * 16);
   }
   {
-    const int t = min(lane & 31, nvalid - 1);
-    const uint16_t* src = ((lane < 32) ? s.vs : s.vm) + o.vm + (int64_t)(t0 + t) * (HD / 32);
+    const int t = min(ts + (tid & (kStage - 1)), t_last);
+    const uint16_t* m = ((tid < kStage) ? s.vs : s.vm) + o.vm + (int64_t)t * (HD / 32);
     if (HD == 128) {
-      const u2_t x = *reinterpret_cast<const u2_t*>(src);
-      r.vmeta[0] = x[0];
-      r.vmeta[HD / 64 - 1] = x[1];
+      r.vm = *reinterpret_cast<const u2_t*>(m);
     } else {
-      r.vmeta[0] = *reinterpret_cast<const uint32_t*>(src);
+      r.vm = u2_t{*reinterpret_cast<const uint32_t*>(m), 0u};
     }
   }
 }
 
 template <int HD, int KB, int VB>
-__device__ __forceinline__ void store_group(const GroupRegs<HD, KB, VB>& r, const SegDev& s,
-                                            const SegOffsets& o, bool kfast, int t0, int lane,
-                                            char* lds) {
-  using L = KiviLayout<HD, KB, VB>;
-  using R = GroupRegs<HD, KB, VB>;
-  uint32_t* kw = reinterpret_cast<uint32_t*>(lds);
-  if (kfast) {
+__device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, int tid, char* st) {
+  using L = StageLayout<HD, KB, VB>;
+  using R = StageRegs<HD, KB, VB>;
+  uint32_t* kw = reinterpret_cast<uint32_t*>(st);
 #pragma unroll
-    for (int i = 0; i < R::NK; ++i) {
-      const int q = lane + 64 * i;
-      const int c = q / R::KCR, u = q - c * R::KCR;
-      constexpr int W = R::KCB / 4;
+  for (int i = 0; i < R::NK; ++i) {
+    const int q = tid + kThreads * i;
+    if (R::KP % kThreads == 0 || q < R::KP) {
+      const int c = q / KB, j = q - c * KB;
 #pragma unroll
-      for (int k = 0; k < W; ++k) kw[(W * u + k) * L::kw_row + c] = r.k[i][k];
-    }
-  } else {
-    // rows that are not a multiple of the load width (short segments): 4 or 1 bytes at a time
-    const int64_t row_bytes = ((int64_t)s.length * KB + 7) / 8;
-    const int64_t byte0 = (int64_t)t0 * KB / 8;
-    const uint8_t* krow0 = s.kd + o.kd;
-    const bool dw = (row_bytes & 3) == 0;
-    for (int q = lane; q < HD * KB; q += 64) {
-      const int c = q / KB, w = q - c * KB;
-      const int64_t off = byte0 + 4 * w;
-      uint32_t v = 0u;
-      if (dw) {
-        if (off < row_bytes) v = *reinterpret_cast<const uint32_t*>(krow0 + c * row_bytes + off);
-      } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (off + k < row_bytes) v |= (uint32_t)krow0[c * row_bytes + off + k] << (8 * k);
-      }
-      kw[w * L::kw_row + c] = v;
+      for (int w = 0; w < 4; ++w) kw[(4 * j + w) * L::kw_row + c] = r.k[i][w];
     }
   }
-  uint16_t* ks = reinterpret_cast<uint16_t*>(lds + L::off_ks);
-  uint16_t* km = reinterpret_cast<uint16_t*>(lds + L::off_km);
+  if (tid < 2 * HD) {
+    uint16_t* m = reinterpret_cast<uint16_t*>(st + ((tid < HD) ? L::off_ks : L::off_km));
+    const int c = tid % HD;
 #pragma unroll
-  for (int i = 0; i < R::NKM; ++i) {
-    ks[lane + 64 * i] = r.ks[i];
-    km[lane + 64 * i] = r.km[i];
+    for (int g = 0; g < 4; ++g) m[g * HD + c] = (uint16_t)(r.km[g >> 1] >> (16 * (g & 1)));
   }
-  u4_t* vw = reinterpret_cast<u4_t*>(lds + L::off_vw);
+  u4_t* vw = reinterpret_cast<u4_t*>(st + L::off_vw);
 #pragma unroll
-  for (int i = 0; i < R::NV; ++i)
-    if (lane + 64 * i < R::VCH) vw[lane + 64 * i] = r.v[i];
-  // V metadata: token-major in global, channel-group-major in LDS
-  uint16_t* vmeta = reinterpret_cast<uint16_t*>(lds + ((lane < 32) ? L::off_vs : L::off_vm));
-  const int t = lane & 31;
+  for (int i = 0; i < R::NV; ++i) {
+    const int q = tid + kThreads * i;
+    if (R::VP % kThreads == 0 || q < R::VP) vw[q] = r.v[i];
+  }
+  {
+    uint16_t* m = reinterpret_cast<uint16_t*>(st + ((tid < kStage) ? L::off_vs : L::off_vm));
+    const int t = tid & (kStage - 1);
 #pragma unroll
-  for (int cg = 0; cg < HD / 32; ++cg)
-    vmeta[cg * kTile + t] = (uint16_t)(r.vmeta[cg >> 1] >> (16 * (cg & 1)));
+    for (int cg = 0; cg < HD / 32; ++cg)
+      m[cg * kStage + t] = (uint16_t)(r.vm[cg >> 1] >> (16 * (cg & 1)));
+  }
 }
 
 // token (within the group) of QK result row rr of instance h
@@ -325,28 +329,32 @@ __device__ __forceinline__ int pv_slot(int h, int e) {
 // one staged 32-token KIVI group
 // ---------------------------------------------------------------------------
 template <int HD, int KB, int VB, bool FULL>
-__device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD / 8],
+__device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, const u4_t (&qb)[HD / 32],
                            WaveAcc<HD>& acc, float sl2, int lane) {
-  using L = KiviLayout<HD, KB, VB>;
+  using L = StageLayout<HD, KB, VB>;
+  const char* kwg = st + grp * KB * L::kw_row * 4;        // the group's Kw rows
+  const char* ksg = st + L::off_ks + grp * HD * 2;
+  const char* kmg = st + L::off_km + grp * HD * 2;
+  const char* vsg = st + L::off_vs + grp * kTile * 2;     // channel group stride kStage
+  const char* vmg = st + L::off_vm + grp * kTile * 2;
   constexpr int KS = HD / 32;
   constexpr int NB = HD / 16;
   constexpr int CG = HD / 32;
   const int r = lane & 15;     // A row (token row) / B column (head)
   const int g4 = lane >> 4;
-  // ---- q folded with the group's K scale, and the K-min bias ----
+  // ---- q folded with the group's K scale; the K-min bias sum_c q mK on the
+  // matrix cores (every A row holds the mins, so every result row is the bias) ----
   u4_t qp[KS];
-  float bpart = 0.f;
+  f4_t db = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    const u4_t sc8 = lds_u4(lds + L::off_ks + (32 * s + 8 * g4) * 2);
-    const u4_t mn8 = lds_u4(lds + L::off_km + (32 * s + 8 * g4) * 2);
+    const u4_t sc8 = lds_u4(ksg + (32 * s + 8 * g4) * 2);
+    const u4_t mn8 = lds_u4(kmg + (32 * s + 8 * g4) * 2);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      qp[s][m] = pkmul(qh[s * 4 + m], sc8[m]);
-      bpart = dot2(qh[s * 4 + m], mn8[m], bpart);
-    }
+    for (int m = 0; m < 4; ++m) qp[s][m] = pkmul(qb[s][m], sc8[m]);
+    db = mfma(mn8, qb[s], db);
   }
-  const float bias = xsum4(bpart) * sl2;
+  const float bias = db[0] * sl2;
   // ---- S^T = codes_K * q' for instances h = 0, 1 (16 tokens each) ----
   f4_t d[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   if constexpr (KB == 8) {
@@ -356,8 +364,8 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
       for (int h = 0; h < 2; ++h) {
         const int w = 4 * h + (r >> 2);
         const uint32_t sel = sel_bytes(r & 3);
-        const u4_t w0 = lds_u4(lds + (w * L::kw_row + 32 * s + 8 * g4) * 4);
-        const u4_t w1 = lds_u4(lds + (w * L::kw_row + 32 * s + 8 * g4 + 4) * 4);
+        const u4_t w0 = lds_u4(kwg + (w * L::kw_row + 32 * s + 8 * g4) * 4);
+        const u4_t w1 = lds_u4(kwg + (w * L::kw_row + 32 * s + 8 * g4 + 4) * 4);
         u4_t a;
         a[0] = perm(w0[1], w0[0], sel);
         a[1] = perm(w0[3], w0[2], sel);
@@ -379,8 +387,8 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
     }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const u4_t w0 = lds_u4(lds + (w * L::kw_row + 32 * s + 8 * g4) * 4);
-      const u4_t w1 = lds_u4(lds + (w * L::kw_row + 32 * s + 8 * g4 + 4) * 4);
+      const u4_t w0 = lds_u4(kwg + (w * L::kw_row + 32 * s + 8 * g4) * 4);
+      const u4_t w1 = lds_u4(kwg + (w * L::kw_row + 32 * s + 8 * g4 + 4) * 4);
       uint32_t u[4];
       u[0] = perm(w0[1], w0[0], sel);
       u[1] = perm(w0[3], w0[2], sel);
@@ -434,15 +442,15 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
   for (int c = 0; c < CG; ++c) {
     u4_t sv, mv;
     if constexpr (KB == 8) {
-      const u2_t s0 = lds_u2(lds + L::off_vs + (c * kTile + 4 * g4) * 2);
-      const u2_t s1 = lds_u2(lds + L::off_vs + (c * kTile + 16 + 4 * g4) * 2);
-      const u2_t m0 = lds_u2(lds + L::off_vm + (c * kTile + 4 * g4) * 2);
-      const u2_t m1 = lds_u2(lds + L::off_vm + (c * kTile + 16 + 4 * g4) * 2);
+      const u2_t s0 = lds_u2(vsg + (c * kStage + 4 * g4) * 2);
+      const u2_t s1 = lds_u2(vsg + (c * kStage + 16 + 4 * g4) * 2);
+      const u2_t m0 = lds_u2(vmg + (c * kStage + 4 * g4) * 2);
+      const u2_t m1 = lds_u2(vmg + (c * kStage + 16 + 4 * g4) * 2);
       sv = u4_t{s0[0], s0[1], s1[0], s1[1]};
       mv = u4_t{m0[0], m0[1], m1[0], m1[1]};
     } else {
-      sv = lds_u4(lds + L::off_vs + (c * kTile + 8 * g4) * 2);
-      mv = lds_u4(lds + L::off_vm + (c * kTile + 8 * g4) * 2);
+      sv = lds_u4(vsg + (c * kStage + 8 * g4) * 2);
+      mv = lds_u4(vmg + (c * kStage + 8 * g4) * 2);
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -452,7 +460,7 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
   }
   // ---- O^T += codes_V^T * P' : channel block b, row r <-> channel 16 b + r ----
   constexpr int RW = L::vrow_words;
-  const char* vw = lds + L::off_vw;
+  const char* vw = st + L::off_vw + grp * kTile * L::vrow_bytes;
   int tok[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) tok[j] = pv_token<KB>(g4, j);
@@ -518,7 +526,7 @@ __device__ void kivi_group(int nvalid, const char* lds, const uint32_t (&qh)[HD 
 // masked scores (K) or p = 0 weights (V).
 // ---------------------------------------------------------------------------
 template <int HD>
-__device__ void fp16_group(const uint16_t* kbase, const uint16_t* vbase, int64_t tok_stride,
+__device__ __forceinline__ void fp16_group(const uint16_t* kbase, const uint16_t* vbase, int64_t tok_stride,
                            int t0, int nvalid, const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
                            float sl2, int lane) {
   constexpr int KS = HD / 32;
@@ -594,27 +602,61 @@ __device__ void fp16_group(const uint16_t* kbase, const uint16_t* vbase, int64_t
 // ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
+// Every wave of the workgroup runs this with the same arguments (the stage
+// barriers are workgroup-wide).  Stage i lives in LDS buffer i % 2; while the
+// waves compute it, the loads of the next DEPTH stages are in flight in
+// registers.  Wave w computes group w of each stage.
 template <int HD, int KB, int VB>
-__device__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_begin, int t_end, int wave,
-                           int lane, char* lds_wave, const uint32_t (&qh)[HD / 8],
-                           WaveAcc<HD>& acc, float sl2) {
-  int t0 = t_begin + kTile * wave;
-  if (t0 >= t_end) return;
-  using R = GroupRegs<HD, KB, VB>;
-  const bool kfast = ((((int64_t)s.length * KB + 7) / 8) % R::KCB) == 0;
-  R regs;
-  load_group<HD, KB, VB>(regs, s, o, kfast, t0, min(kTile, t_end - t0), lane);
-  for (;;) {
-    const int nvalid = min(kTile, t_end - t0);
-    store_group<HD, KB, VB>(regs, s, o, kfast, t0, lane, lds_wave);
-    __builtin_amdgcn_wave_barrier();
-    const int t_next = t0 + kTile * kWaves;
-    if (t_next < t_end) load_group<HD, KB, VB>(regs, s, o, kfast, t_next, min(kTile, t_end - t_next), lane);
-    if (nvalid == kTile) kivi_group<HD, KB, VB, true>(nvalid, lds_wave, qh, acc, sl2, lane);
-    else kivi_group<HD, KB, VB, false>(nvalid, lds_wave, qh, acc, sl2, lane);
-    __builtin_amdgcn_wave_barrier();
-    if (t_next >= t_end) break;
-    t0 = t_next;
+__device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_begin,
+                                           int t_end, int wave,
+                           int lane, int tid, char* lds, int stage_bytes,
+                           const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc, float sl2) {
+  using R = StageRegs<HD, KB, VB>;
+  constexpr int DEPTH = (KB + VB <= 8) ? 2 : 1;
+  KivLoad kl;
+  kl.row_bytes = ((int64_t)s.length * KB + 7) / 8;
+  kl.row_groups = (s.length + s.kgs - 1) / s.kgs;
+  const int64_t byte_begin = (int64_t)(t_begin - 0) * KB / 8;
+  const uintptr_t kaddr = reinterpret_cast<uintptr_t>(s.kd + o.kd);
+  if (kl.row_bytes % 16 == 0 && byte_begin % 16 == 0 && kaddr % 16 == 0) kl.kmode = 16;
+  else if (kl.row_bytes % 4 == 0 && byte_begin % 4 == 0 && kaddr % 4 == 0) kl.kmode = 4;
+  else kl.kmode = 1;
+  kl.kmeta4 = (kl.row_groups % 4 == 0) && (t_begin % kStage == 0) &&
+              (reinterpret_cast<uintptr_t>(s.ks + o.km) % 8 == 0) &&
+              (reinterpret_cast<uintptr_t>(s.km + o.km) % 8 == 0);
+  const int t_last = t_end - 1;
+  const int nst = (t_end - t_begin + kStage - 1) / kStage;
+  char* buf0 = lds;
+  char* buf1 = lds + stage_bytes;
+  // stages 0, 2, 4, ... pass through ra, stages 1, 3, 5, ... through rb (DEPTH 2)
+  R ra, rb;
+  load_stage<HD, KB, VB>(ra, s, o, kl, t_begin, t_last, tid);
+  if (DEPTH == 2 && nst > 1) load_stage<HD, KB, VB>(rb, s, o, kl, t_begin + kStage, t_last, tid);
+  store_stage<HD, KB, VB>(ra, tid, buf0);
+  if (nst > DEPTH) load_stage<HD, KB, VB>(ra, s, o, kl, t_begin + DEPTH * kStage, t_last, tid);
+  __syncthreads();
+  for (int i = 0; i < nst; ++i) {
+    const int t0 = t_begin + i * kStage + kTile * wave;
+    if (t0 < t_end) {
+      const char* st = (i & 1) ? buf1 : buf0;
+      const int nvalid = min(kTile, t_end - t0);
+      if (nvalid == kTile) kivi_group<HD, KB, VB, true>(nvalid, st, wave, qb, acc, sl2, lane);
+      else kivi_group<HD, KB, VB, false>(nvalid, st, wave, qb, acc, sl2, lane);
+    }
+    if (i + 1 < nst) {
+      // stage i + 1 into the other buffer, whose last readers (stage i - 1)
+      // all passed the previous barrier; then the loads of stage i + 1 + DEPTH
+      char* nb = (i & 1) ? buf0 : buf1;
+      const int tn = t_begin + (i + 1 + DEPTH) * kStage;
+      if (DEPTH == 1 || !(i & 1)) {
+        store_stage<HD, KB, VB>(DEPTH == 1 ? ra : rb, tid, nb);
+        if (i + 1 + DEPTH < nst) load_stage<HD, KB, VB>(DEPTH == 1 ? ra : rb, s, o, kl, tn, t_last, tid);
+      } else {
+        store_stage<HD, KB, VB>(ra, tid, nb);
+        if (i + 1 + DEPTH < nst) load_stage<HD, KB, VB>(ra, s, o, kl, tn, t_last, tid);
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -657,16 +699,11 @@ decode_mfma_kernel(const DecodeParams p) {
   // repeat the slab's last head; their results are never written, and the
   // loads stay unconditional so they do not serialize with the first group's.
   u4_t qb[KS];
-  uint32_t qh[HD / 8];
   const int nq = min(n, nh - 1);
 #pragma unroll
-  for (int k = 0; k < KS; ++k) {
-    const u4_t v = *reinterpret_cast<const u4_t*>(p.q + (int64_t)b * p.q_bs +
-                                                  (int64_t)(h0 + nq) * p.q_hs + 32 * k + 8 * g4);
-    qb[k] = v;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) qh[4 * k + m] = v[m];
-  }
+  for (int k = 0; k < KS; ++k)
+    qb[k] = *reinterpret_cast<const u4_t*>(p.q + (int64_t)b * p.q_bs + (int64_t)(h0 + nq) * p.q_hs +
+                                           32 * k + 8 * g4);
 
   WaveAcc<HD> acc;
 #pragma unroll
@@ -677,7 +714,6 @@ decode_mfma_kernel(const DecodeParams p) {
   acc.mx = -INFINITY;
   acc.l = 0.f;
 
-  char* lds_wave = lds + wave * p.wave_lds;
   if (s.kind == PK_SEG_FP16) {
     const uint16_t* kbase = reinterpret_cast<const uint16_t*>(s.kd) + b * s.kd_bs + kvh * s.kd_hs;
     const uint16_t* vbase = reinterpret_cast<const uint16_t*>(s.vd) + b * s.vd_bs + kvh * s.vd_hs;
@@ -694,7 +730,8 @@ decode_mfma_kernel(const DecodeParams p) {
 #define PK_KIVI_CASE(KB_, VB_)                                                                 \
   if constexpr (KB_ <= MAXB && VB_ <= MAXB) {                                                  \
     if (s.kbits == KB_ && s.vbits == VB_)                                                      \
-      kivi_chunk<HD, KB_, VB_>(s, o, t_begin, t_end, wave, lane, lds_wave, qh, acc, sl2);      \
+      kivi_chunk<HD, KB_, VB_>(s, o, t_begin, t_end, wave, lane, tid, lds, p.stage_lds, qb, acc, \
+                               sl2);                                                           \
   }
     PK_KIVI_CASE(2, 2) PK_KIVI_CASE(2, 4) PK_KIVI_CASE(2, 8)
     PK_KIVI_CASE(4, 2) PK_KIVI_CASE(4, 4) PK_KIVI_CASE(4, 8)
@@ -776,17 +813,24 @@ decode_mfma_kernel(const DecodeParams p) {
 
 }  // namespace
 
-// LDS bytes per wave for the largest K / V bit widths of a launch
-static int kivi_wave_bytes(int hd, int kb, int vb) {
-  return 4 * (hd + 8) * kb + 4 * hd * (vb + 2);
+// LDS bytes of one stage buffer for the largest K / V bit widths of a launch
+static int kivi_stage_bytes(int hd, int kb, int vb) {
+  if (hd == 128) {
+    if (kb == 8 || vb == 8) return StageLayout<128, 8, 8>::bytes;
+    if (kb == 4 || vb == 4) return StageLayout<128, 4, 4>::bytes;
+    return StageLayout<128, 2, 2>::bytes;
+  }
+  if (kb == 8 || vb == 8) return StageLayout<64, 8, 8>::bytes;
+  if (kb == 4 || vb == 4) return StageLayout<64, 4, 4>::bytes;
+  return StageLayout<64, 2, 2>::bytes;
 }
 
 int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, int max_vbits,
                        hipStream_t stream) {
   DecodeParams dp = dp_in;
   const int hd = dp.hd;
-  dp.wave_lds = (kivi_wave_bytes(hd, max_kbits, max_vbits) + 15) & ~15;
-  const size_t staging = (size_t)kWaves * dp.wave_lds;
+  dp.stage_lds = (kivi_stage_bytes(hd, max_kbits, max_vbits) + 15) & ~15;
+  const size_t staging = 2 * (size_t)dp.stage_lds;
   const size_t merge = sizeof(float) * ((size_t)kWaves * 16 * hd + 2 * kWaves * 16);
   const size_t lds = std::max(staging, merge);
   dim3 grid(lchunks, dp.Hkv * dp.nslab, dp.B);
