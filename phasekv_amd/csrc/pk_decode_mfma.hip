@@ -259,6 +259,52 @@ __device__ __forceinline__ void load_stage(StageRegs<HD, KB, VB>& r, const SegDe
   }
 }
 
+// Per-lane offsets of the fast stage loads, fixed for a segment.
+template <int HD, int KB, int VB>
+struct FastOffsets {
+  uint32_t krow[StageRegs<HD, KB, VB>::NK];   // channel row start of each K piece
+  uint32_t mrow;                             // K metadata: channel row start (elements)
+};
+
+// Stage loads for segments whose K rows are 16-byte aligned and hold a
+// multiple of 128 tokens' K groups: every lane issues the same loads, with no
+// predicate and no branch, so the compiler's wait counts stay exact and the
+// next stages' loads are not waited for.  Lanes without a piece of their own
+// (head_dim 64) load a neighbour's, which the store skips.
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void load_stage_fast(StageRegs<HD, KB, VB>& r, const SegDev& s,
+                                                const SegOffsets& o, const KivLoad& kl,
+                                                const FastOffsets<HD, KB, VB>& fo, int ts,
+                                                int t_last, int tid) {
+  using R = StageRegs<HD, KB, VB>;
+  using L = StageLayout<HD, KB, VB>;
+  const uint32_t byte0 = (uint32_t)ts * KB / 8;
+  const uint32_t kmax = (uint32_t)kl.row_bytes - 16;
+  const uint8_t* krows = s.kd + o.kd;
+#pragma unroll
+  for (int i = 0; i < R::NK; ++i) {
+    const uint32_t kj = 16u * ((tid + kThreads * i) % KB);   // piece within the row span
+    r.k[i] = *reinterpret_cast<const u4_t*>(krows + fo.krow[i] + min(byte0 + kj, kmax));
+  }
+  {
+    const uint16_t* m = ((tid & (2 * HD - 1)) < HD ? s.ks : s.km) + o.km;
+    r.km = *reinterpret_cast<const u2_t*>(m + fo.mrow + ts / 32);
+  }
+  const int last_piece = (t_last - ts + 1) * (L::vrow_bytes / 16) - 1;
+  const uint8_t* vsrc = s.vd + o.vd + (int64_t)ts * L::vrow_bytes;
+#pragma unroll
+  for (int i = 0; i < R::NV; ++i) {
+    const int q = (tid + kThreads * i) & (R::VP - 1);
+    r.v[i] = *reinterpret_cast<const u4_t*>(vsrc + min(q, last_piece) * 16);
+  }
+  {
+    const int t = min(ts + (tid & (kStage - 1)), t_last);
+    const uint16_t* m = ((tid < kStage) ? s.vs : s.vm) + o.vm + (int64_t)t * (HD / 32);
+    if (HD == 128) r.vm = *reinterpret_cast<const u2_t*>(m);
+    else r.vm = u2_t{*reinterpret_cast<const uint32_t*>(m), 0u};
+  }
+}
+
 template <int HD, int KB, int VB>
 __device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, int tid, char* st) {
   using L = StageLayout<HD, KB, VB>;
@@ -602,21 +648,114 @@ __device__ __forceinline__ void fp16_group(const uint16_t* kbase, const uint16_t
 // ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
+// one 32-token group of stage i (wave w computes group w of each stage)
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void stage_group(const char* st, int i, int t_begin, int t_end,
+                                            int wave, int lane, const u4_t (&qb)[HD / 32],
+                                            WaveAcc<HD>& acc, float sl2) {
+  const int t0 = t_begin + i * kStage + kTile * wave;
+  if (t0 < t_end) {
+    const int nvalid = min(kTile, t_end - t0);
+    if (nvalid == kTile) kivi_group<HD, KB, VB, true>(nvalid, st, wave, qb, acc, sl2, lane);
+    else kivi_group<HD, KB, VB, false>(nvalid, st, wave, qb, acc, sl2, lane);
+  }
+}
+
 // Every wave of the workgroup runs this with the same arguments (the stage
 // barriers are workgroup-wide).  Stage i lives in LDS buffer i % 2; while the
 // waves compute it, the loads of the next DEPTH stages are in flight in
-// registers.  Wave w computes group w of each stage.
+// registers (stages 0, 2, 4, ... in ra, 1, 3, 5, ... in rb when DEPTH is 2).
+// FAST: the unconditional loads of load_stage_fast, in a steady-state loop
+// unrolled so that each half uses one register set; the compiler then waits
+// only for the stage it stores.  Otherwise the general loads of load_stage.
+template <int HD, int KB, int VB, bool FAST>
+__device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o,
+                                            const KivLoad& kl, int t_begin, int t_end, int wave,
+                                            int lane, int tid, char* lds, int stage_bytes,
+                                            const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
+                                            float sl2) {
+  using R = StageRegs<HD, KB, VB>;
+  constexpr int DEPTH = (KB + VB <= 4) ? 2 : 1;
+  const int t_last = t_end - 1;
+  const int nst = (t_end - t_begin + kStage - 1) / kStage;
+  FastOffsets<HD, KB, VB> fo;
+  if constexpr (FAST) {
+#pragma unroll
+    for (int i = 0; i < R::NK; ++i) {
+      const int q = (tid + kThreads * i) & (R::KP - 1);
+      fo.krow[i] = (uint32_t)((q / KB) * kl.row_bytes);
+    }
+    fo.mrow = (uint32_t)((tid & (HD - 1)) * kl.row_groups);
+  }
+  auto load = [&](R& r, int st) {
+    if constexpr (FAST) load_stage_fast<HD, KB, VB>(r, s, o, kl, fo, t_begin + st * kStage, t_last, tid);
+    else load_stage<HD, KB, VB>(r, s, o, kl, t_begin + st * kStage, t_last, tid);
+  };
+  char* buf0 = lds;
+  char* buf1 = lds + stage_bytes;
+  R ra, rb;
+  int i = 0;
+  if constexpr (DEPTH == 2) {
+    load(ra, 0);
+    if (nst > 1) load(rb, 1);
+    store_stage<HD, KB, VB>(ra, tid, buf0);
+    if (nst > 2) load(ra, 2);
+    __syncthreads();
+    // steady state: stages i + 1 and i + 2 in flight, i + 3 and i + 4 loaded here
+    for (; i + 4 < nst; i += 2) {
+      stage_group<HD, KB, VB>(buf0, i, t_begin, t_end, wave, lane, qb, acc, sl2);
+      store_stage<HD, KB, VB>(rb, tid, buf1);
+      load(rb, i + 3);
+      __syncthreads();
+      stage_group<HD, KB, VB>(buf1, i + 1, t_begin, t_end, wave, lane, qb, acc, sl2);
+      store_stage<HD, KB, VB>(ra, tid, buf0);
+      load(ra, i + 4);
+      __syncthreads();
+    }
+    // tail: at most four stages left, none loaded beyond nst
+    for (; i < nst; ++i) {
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_begin, t_end, wave, lane, qb, acc, sl2);
+      if (i + 1 < nst) {
+        if (i & 1) {
+          store_stage<HD, KB, VB>(ra, tid, buf0);
+          if (i + 3 < nst) load(ra, i + 3);
+        } else {
+          store_stage<HD, KB, VB>(rb, tid, buf1);
+          if (i + 3 < nst) load(rb, i + 3);
+        }
+        __syncthreads();
+      }
+    }
+  } else {
+    load(ra, 0);
+    store_stage<HD, KB, VB>(ra, tid, buf0);
+    if (nst > 1) load(ra, 1);
+    __syncthreads();
+    for (; i + 2 < nst; ++i) {
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_begin, t_end, wave, lane, qb, acc, sl2);
+      store_stage<HD, KB, VB>(ra, tid, (i & 1) ? buf0 : buf1);
+      load(ra, i + 2);
+      __syncthreads();
+    }
+    for (; i < nst; ++i) {
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_begin, t_end, wave, lane, qb, acc, sl2);
+      if (i + 1 < nst) {
+        store_stage<HD, KB, VB>(ra, tid, (i & 1) ? buf0 : buf1);
+        __syncthreads();
+      }
+    }
+  }
+}
+
 template <int HD, int KB, int VB>
 __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_begin,
-                                           int t_end, int wave,
-                           int lane, int tid, char* lds, int stage_bytes,
-                           const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc, float sl2) {
-  using R = StageRegs<HD, KB, VB>;
-  constexpr int DEPTH = (KB + VB <= 8) ? 2 : 1;
+                                           int t_end, int wave, int lane, int tid, char* lds,
+                                           int stage_bytes, const u4_t (&qb)[HD / 32],
+                                           WaveAcc<HD>& acc, float sl2) {
   KivLoad kl;
   kl.row_bytes = ((int64_t)s.length * KB + 7) / 8;
   kl.row_groups = (s.length + s.kgs - 1) / s.kgs;
-  const int64_t byte_begin = (int64_t)(t_begin - 0) * KB / 8;
+  const int64_t byte_begin = (int64_t)t_begin * KB / 8;
   const uintptr_t kaddr = reinterpret_cast<uintptr_t>(s.kd + o.kd);
   if (kl.row_bytes % 16 == 0 && byte_begin % 16 == 0 && kaddr % 16 == 0) kl.kmode = 16;
   else if (kl.row_bytes % 4 == 0 && byte_begin % 4 == 0 && kaddr % 4 == 0) kl.kmode = 4;
@@ -624,40 +763,12 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
   kl.kmeta4 = (kl.row_groups % 4 == 0) && (t_begin % kStage == 0) &&
               (reinterpret_cast<uintptr_t>(s.ks + o.km) % 8 == 0) &&
               (reinterpret_cast<uintptr_t>(s.km + o.km) % 8 == 0);
-  const int t_last = t_end - 1;
-  const int nst = (t_end - t_begin + kStage - 1) / kStage;
-  char* buf0 = lds;
-  char* buf1 = lds + stage_bytes;
-  // stages 0, 2, 4, ... pass through ra, stages 1, 3, 5, ... through rb (DEPTH 2)
-  R ra, rb;
-  load_stage<HD, KB, VB>(ra, s, o, kl, t_begin, t_last, tid);
-  if (DEPTH == 2 && nst > 1) load_stage<HD, KB, VB>(rb, s, o, kl, t_begin + kStage, t_last, tid);
-  store_stage<HD, KB, VB>(ra, tid, buf0);
-  if (nst > DEPTH) load_stage<HD, KB, VB>(ra, s, o, kl, t_begin + DEPTH * kStage, t_last, tid);
-  __syncthreads();
-  for (int i = 0; i < nst; ++i) {
-    const int t0 = t_begin + i * kStage + kTile * wave;
-    if (t0 < t_end) {
-      const char* st = (i & 1) ? buf1 : buf0;
-      const int nvalid = min(kTile, t_end - t0);
-      if (nvalid == kTile) kivi_group<HD, KB, VB, true>(nvalid, st, wave, qb, acc, sl2, lane);
-      else kivi_group<HD, KB, VB, false>(nvalid, st, wave, qb, acc, sl2, lane);
-    }
-    if (i + 1 < nst) {
-      // stage i + 1 into the other buffer, whose last readers (stage i - 1)
-      // all passed the previous barrier; then the loads of stage i + 1 + DEPTH
-      char* nb = (i & 1) ? buf0 : buf1;
-      const int tn = t_begin + (i + 1 + DEPTH) * kStage;
-      if (DEPTH == 1 || !(i & 1)) {
-        store_stage<HD, KB, VB>(DEPTH == 1 ? ra : rb, tid, nb);
-        if (i + 1 + DEPTH < nst) load_stage<HD, KB, VB>(DEPTH == 1 ? ra : rb, s, o, kl, tn, t_last, tid);
-      } else {
-        store_stage<HD, KB, VB>(ra, tid, nb);
-        if (i + 1 + DEPTH < nst) load_stage<HD, KB, VB>(ra, s, o, kl, tn, t_last, tid);
-      }
-      __syncthreads();
-    }
-  }
+  if (kl.kmode == 16 && kl.kmeta4 && kl.row_bytes < ((int64_t)1 << 31) / HD)
+    kivi_stages<HD, KB, VB, true>(s, o, kl, t_begin, t_end, wave, lane, tid, lds, stage_bytes, qb,
+                                  acc, sl2);
+  else
+    kivi_stages<HD, KB, VB, false>(s, o, kl, t_begin, t_end, wave, lane, tid, lds, stage_bytes,
+                                   qb, acc, sl2);
 }
 
 // Two workgroups (8 waves) per CU: the register budget is capped so a second
