@@ -696,9 +696,11 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
   R ra, rb;
   int i = 0;
   if constexpr (DEPTH == 2) {
+    // stage 0 goes out alone: every workgroup starts at once, and its first
+    // stage should not queue behind everybody's next ones
     load(ra, 0);
-    if (nst > 1) load(rb, 1);
     store_stage<HD, KB, VB>(ra, tid, buf0);
+    if (nst > 1) load(rb, 1);
     if (nst > 2) load(ra, 2);
     __syncthreads();
     // steady state: stages i + 1 and i + 2 in flight, i + 3 and i + 4 loaded here
@@ -867,58 +869,61 @@ decode_mfma_kernel(const DecodeParams p) {
   float* ml = mm + kWaves * 16;                             // [4][16]
   const float l_full = xsum4(acc.l);
   if (s.kind == PK_SEG_FP16) {
+    // result row r of block bb is channel NB r + bb: 8 consecutive channels per (g4, e)
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb)
+    for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        mo[(wave * 16 + n) * HD + NB * (4 * g4 + e) + bb] = acc.o[bb][e];
+      for (int bb = 0; bb < NB; bb += 4)
+        *reinterpret_cast<f4_t*>(mo + (wave * 16 + n) * HD + NB * (4 * g4 + e) + bb) =
+            f4_t{acc.o[bb][e], acc.o[bb + 1][e], acc.o[bb + 2][e], acc.o[bb + 3][e]};
   } else {
     float vbf[HD / 32];
 #pragma unroll
     for (int c = 0; c < HD / 32; ++c) vbf[c] = xsum4(acc.vb[c]);
     // V code position factor of result row 4 g4 + e
     const int vb_bits = s.vbits;
+    f4_t f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      f[e] = kTwo24 / ((vb_bits == 2) ? (float)(1 << (2 * e)) : (vb_bits == 4) ? ((e & 1) ? 16.f : 1.f) : 1.f);
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float pos = (vb_bits == 2) ? (float)(1 << (2 * e))
-                          : (vb_bits == 4) ? ((e & 1) ? 16.f : 1.f) : 1.f;
-        mo[(wave * 16 + n) * HD + 16 * bb + 4 * g4 + e] =
-            acc.o[bb][e] * (kTwo24 / pos) + vbf[bb >> 1];
-      }
+      *reinterpret_cast<f4_t*>(mo + (wave * 16 + n) * HD + 16 * bb + 4 * g4) =
+          acc.o[bb] * f + vbf[bb >> 1];
   }
   if (g4 == 0) {
     mm[wave * 16 + n] = acc.m;
     ml[wave * 16 + n] = l_full;
   }
   __syncthreads();
-  for (int i = tid; i < nh * HD; i += 256) {
-    const int hh = i / HD, c = i - hh * HD;
+  // thread -> (head, 4 channels): the four waves' weights once per head, then
+  // one 16-byte read per wave and one 16-byte store
+  constexpr int Q = HD / 4;
+  for (int i = tid; i < nh * Q; i += 256) {
+    const int hh = i / Q, c = 4 * (i - hh * Q);
+    float mw[kWaves];
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mm[w * 16 + hh]);
-    float o = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w)
-        o += __builtin_amdgcn_exp2f(mm[w * 16 + hh] - M) * mo[(w * 16 + hh) * HD + c];
+    for (int w = 0; w < kWaves; ++w) {
+      mw[w] = mm[w * 16 + hh];
+      M = fmaxf(M, mw[w]);
     }
-    const int64_t row = (int64_t)b * p.Hq + h0 + hh;
-    p.ws_acc[(row * p.C + cg) * HD + c] = o;
-  }
-  for (int hh = tid; hh < nh; hh += 256) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mm[w * 16 + hh]);
+    f4_t o = {0.f, 0.f, 0.f, 0.f};
     float L = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) L += __builtin_amdgcn_exp2f(mm[w * 16 + hh] - M) * ml[w * 16 + hh];
+      for (int w = 0; w < kWaves; ++w) {
+        const float wt = __builtin_amdgcn_exp2f(mw[w] - M);
+        o += wt * *reinterpret_cast<const f4_t*>(mo + (w * 16 + hh) * HD + c);
+        L += wt * ml[w * 16 + hh];
+      }
     }
     const int64_t row = (int64_t)b * p.Hq + h0 + hh;
-    p.ws_m[row * p.C + cg] = (M == -INFINITY) ? -INFINITY : M * kLn2;
-    p.ws_l[row * p.C + cg] = L;
+    *reinterpret_cast<f4_t*>(p.ws_acc + (row * p.C + cg) * HD + c) = o;
+    if (c == 0) {
+      p.ws_m[row * p.C + cg] = (M == -INFINITY) ? -INFINITY : M * kLn2;
+      p.ws_l[row * p.C + cg] = L;
+    }
   }
 }
 
