@@ -19,7 +19,8 @@ counters read for it, from the committed PMC summary.
 
 Prints ONE JSON line (rank 0).  Extra fields: ``us_per_step``, the FP16 dense
 GQA-aware comparator on the same tokens, and ``sweep``: the same measurement
-for the context sweep (C3) and the batched configurations (C4, C5).
+for the context sweep (C3), the batched configurations (C4, C5) and C4's
+prefill-side quantize + pack of an 8192 x 4 x 128 K/V block.
 """
 from __future__ import annotations
 
@@ -118,6 +119,32 @@ def _bench_config(cfg, device, steps, warmup, stream, with_dense=True):
         del sets, probs, dfns, dense
     torch.cuda.empty_cache()
     return res, wl
+
+
+def _bench_prefill_pack(device, steps, warmup, stream):
+    """C4's prefill side: an 8192 x 4 x 128 fp16 K/V block packed to the 2-bit prompt tier.
+
+    K is quantized per channel along tokens (axis -2), V per token along head_dim
+    (axis -1), groups of 32 (``phasekv_cache.py:101-107``).  Algorithmic bytes: the
+    fp16 block read once, packed codes and fp16 scale/min written once.
+    """
+    from phasekv_amd.kernels.packing import quantize_pack
+    gen = torch.Generator().manual_seed(1234)
+    shape = (1, 4, 8192, 128)
+    k = torch.randn(*shape, generator=gen).to(torch.float16).to(device)
+    v = torch.randn(*shape, generator=gen).to(torch.float16).to(device)
+    elems = k.numel()
+    nbytes = 2 * (2 * elems) + 2 * (elems // 4) + 2 * 2 * 2 * (elems // 32)
+    copies = _copies_for(2 * 2 * elems, 64)
+    sets = [(k, v)] + [(k.clone(), v.clone()) for _ in range(copies - 1)]
+    fns = [lambda kv=kv: (quantize_pack(kv[0], 2, -2, 32), quantize_pack(kv[1], 2, -1, 32))
+           for kv in sets]
+    sec = _time_graph(fns, steps, warmup, stream)
+    del sets, fns
+    torch.cuda.empty_cache()
+    return {"config": "C4-prefill-pack", "shape": list(shape), "bits": 2, "bytes": nbytes,
+            "copies": copies, "us_per_step": sec * 1e6, "gbs": nbytes / sec / 1e9,
+            "frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
 
 
 def _cpu_baseline(cfg_name: str, budget_s: float = 10.0):
@@ -226,6 +253,9 @@ def main() -> int:
                                  stream, with_dense=not args.no_dense)
             _log(f"bench: {name} {r}")
             sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+        r = _bench_prefill_pack(device, min(args.steps, 128), min(args.warmup, 128), stream)
+        _log(f"bench: C4-prefill-pack {r}")
+        sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
     cpu = None
     if not args.no_cpu:
         cpu = _cpu_baseline(cfg.name if cfg.batch == 1 else "C2", args.cpu_seconds)

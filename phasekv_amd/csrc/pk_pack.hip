@@ -158,6 +158,111 @@ quantize_groups_kernel(QuantParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fast paths for the cache's own layouts: fp16 input, contiguous, groups of 32.
+// Same arithmetic as group_stats / quant_code, element for element.
+// ---------------------------------------------------------------------------
+typedef uint32_t pk_u4 __attribute__((ext_vector_type(4)));
+
+template <int BITS>
+__device__ __forceinline__ void pack32(const float (&v)[32], const GroupStats& s,
+                                       uint32_t (&w)[BITS]) {
+  constexpr int per = 32 / BITS;            // codes per 32-bit word
+#pragma unroll
+  for (int k = 0; k < BITS; ++k) {
+    uint32_t x = 0;
+#pragma unroll
+    for (int j = 0; j < per; ++j) x |= quant_code(v[k * per + j], s, BITS) << (j * BITS);
+    w[k] = x;
+  }
+}
+
+__device__ __forceinline__ GroupStats stats32(const float (&v)[32], int bits) {
+  float mn = v[0], mx = v[0];
+#pragma unroll
+  for (int i = 1; i < 32; ++i) {
+    mn = nan_min(mn, v[i]);
+    mx = nan_max(mx, v[i]);
+  }
+  float range = __fsub_rn(mx, mn);
+  range = (range < 1e-8f) ? 1e-8f : range;
+  return GroupStats{mn, __fdiv_rn(range, static_cast<float>((1 << bits) - 1))};
+}
+
+// Groups along the contiguous axis (V, per token along head_dim): one thread
+// per (row, group) with the group index fastest, four 16-byte loads, one
+// packed store.
+template <int BITS>
+__global__ void __launch_bounds__(kThreads)
+quantize_inner32_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t len, int64_t ngroups,
+                        int64_t nbytes, uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+                        uint16_t* __restrict__ mins) {
+  const int64_t total = rows * ngroups;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / ngroups, g = i - r * ngroups;
+    const pk_u4* src = reinterpret_cast<const pk_u4*>(x + r * len + g * 32);
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const pk_u4 q = src[k];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[8 * k + 2 * j] = pk_h2f((uint16_t)(q[j] & 0xFFFFu));
+        v[8 * k + 2 * j + 1] = pk_h2f((uint16_t)(q[j] >> 16));
+      }
+    }
+    const GroupStats st = stats32(v, BITS);
+    scale[i] = pk_f2h(st.scale);
+    mins[i] = pk_f2h(st.mn);
+    uint32_t w[BITS];
+    pack32<BITS>(v, st, w);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(packed + r * nbytes + g * 4 * BITS);
+#pragma unroll
+    for (int k = 0; k < BITS; ++k) dst[k] = w[k];
+  }
+}
+
+// Groups along the second-innermost axis with a contiguous innermost dim D
+// (K, per channel along tokens): one thread per (outer, group, channel pair),
+// channel pair fastest, so each load instruction of a wave reads whole token
+// rows; each thread stores two channels' packed group and metadata.
+template <int BITS>
+__global__ void __launch_bounds__(kThreads)
+quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t len, int64_t D,
+                        int64_t ngroups, int64_t nbytes, uint8_t* __restrict__ packed,
+                        uint16_t* __restrict__ scale, uint16_t* __restrict__ mins) {
+  const int64_t pairs = D / 2;
+  const int64_t total = outer * ngroups * pairs;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t cp = i % pairs;
+    const int64_t rest = i / pairs;
+    const int64_t g = rest % ngroups, o = rest / ngroups;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(x + (o * len + g * 32) * D + 2 * cp);
+    float a[32], b[32];
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      const uint32_t q = src[t * (D / 2)];
+      a[t] = pk_h2f((uint16_t)(q & 0xFFFFu));
+      b[t] = pk_h2f((uint16_t)(q >> 16));
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float (&v)[32] = k ? b : a;
+      const GroupStats st = stats32(v, BITS);
+      const int64_t row = o * D + 2 * cp + k;
+      scale[row * ngroups + g] = pk_f2h(st.scale);
+      mins[row * ngroups + g] = pk_f2h(st.mn);
+      uint32_t w[BITS];
+      pack32<BITS>(v, st, w);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(packed + row * nbytes + g * 4 * BITS);
+#pragma unroll
+      for (int j = 0; j < BITS; ++j) dst[j] = w[j];
+    }
+  }
+}
+
 // General group sizes: metadata per (row, group) ...
 __global__ void __launch_bounds__(kThreads)
 quantize_meta_kernel(QuantParams p) {
@@ -317,6 +422,38 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
   p.scale = out_scale;
   p.mins = out_mins;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // the cache's layouts: fp16, contiguous, whole groups of 32 along the last or
+  // second-to-last axis
+  bool contiguous = true;
+  {
+    int64_t expect = 1;
+    for (int d = ndim - 1; d >= 0; --d) {
+      if (shape[d] != 1 && strides[d] != expect) contiguous = false;
+      expect *= shape[d];
+    }
+  }
+  const bool fast = dtype == PK_DTYPE_F16 && contiguous && group_size == 32 && p.len % 32 == 0 &&
+                    reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  if (fast && axis == ndim - 1) {
+    const int64_t groups = p.rows * p.ngroups;
+#define PK_INNER(B) hipLaunchKernelGGL(quantize_inner32_kernel<B>, dim3(grid_for(groups)), dim3(kThreads), \
+                                       0, s, static_cast<const uint16_t*>(x), p.rows, p.len, p.ngroups, \
+                                       p.nbytes, out_packed, out_scale, out_mins)
+    if (bits == 2) PK_INNER(2); else if (bits == 4) PK_INNER(4); else PK_INNER(8);
+#undef PK_INNER
+    return pk::check_launch("quantize_pack");
+  }
+  if (fast && axis == ndim - 2 && shape[ndim - 1] % 2 == 0) {
+    const int64_t D = shape[ndim - 1];
+    const int64_t outer = p.rows / D;
+    const int64_t threads = outer * p.ngroups * (D / 2);
+#define PK_OUTER(B) hipLaunchKernelGGL(quantize_outer32_kernel<B>, dim3(grid_for(threads)), dim3(kThreads), \
+                                       0, s, static_cast<const uint16_t*>(x), outer, p.len, D, p.ngroups, \
+                                       p.nbytes, out_packed, out_scale, out_mins)
+    if (bits == 2) PK_OUTER(2); else if (bits == 4) PK_OUTER(4); else PK_OUTER(8);
+#undef PK_OUTER
+    return pk::check_launch("quantize_pack");
+  }
   if (group_size % (8 / bits) == 0) {
     hipLaunchKernelGGL(quantize_groups_kernel, dim3(grid_for(p.rows * p.ngroups)),
                        dim3(kThreads), 0, s, p);
