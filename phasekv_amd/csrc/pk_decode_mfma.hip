@@ -100,6 +100,13 @@ __device__ __forceinline__ float xmax4(float v) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// One of two uniform base pointers per lane, as an offset select: a select of
+// the pointers themselves can be lowered through a small stack array.
+template <typename T>
+__device__ __forceinline__ const T* pick(bool first, const T* a, const T* b) {
+  return a + (first ? (ptrdiff_t)0 : (b - a));
+}
+
 __device__ __forceinline__ u4_t lds_u4(const char* p) { return *reinterpret_cast<const u4_t*>(p); }
 __device__ __forceinline__ u2_t lds_u2(const char* p) { return *reinterpret_cast<const u2_t*>(p); }
 __device__ __forceinline__ uint32_t lds_u32(const char* p) { return *reinterpret_cast<const uint32_t*>(p); }
@@ -108,10 +115,11 @@ __device__ __forceinline__ uint32_t lds_u32(const char* p) { return *reinterpret
 template <int HD>
 struct WaveAcc {
   f4_t o[HD / 16];     // O^T blocks: rows 4*g4 + e of channel block b, column = head
-  float vb[HD / 32];   // sum_t p * mV  (this lane's tokens)
+  f4_t vbl;            // KIVI: matrix-core accumulator, row c < HD/32 = sum_t p mV of channel
+                       // group c, row HD/32 = sum_t p (rows 4*g4 + e as for o)
   float m;             // reference max of p = 2^(s - m), log2 units, same in the 4 lane groups
   float mx;            // true running max of the scores
-  float l;             // sum_t p (this lane's tokens)
+  float l;             // FP16 segments: sum_t p (this lane's tokens)
 };
 
 // The reference max only moves when a group's max exceeds it by more than
@@ -130,10 +138,9 @@ __device__ __forceinline__ float lazy_rescale(WaveAcc<HD>& acc, float mt) {
     const float alpha = __builtin_amdgcn_exp2f(acc.m - m_new);
     acc.m = m_new;
     acc.l *= alpha;
+    acc.vbl *= alpha;
 #pragma unroll
     for (int b = 0; b < HD / 16; ++b) acc.o[b] *= alpha;
-#pragma unroll
-    for (int c = 0; c < HD / 32; ++c) acc.vb[c] *= alpha;
   }
   return acc.m;
 }
@@ -149,8 +156,14 @@ __device__ __forceinline__ float lazy_rescale(WaveAcc<HD>& acc, float mt) {
 //                                  padding puts the KB pieces a wave stores
 //                                  at once in distinct banks
 //   Ks, Km  fp16 [4][HD]           K scale / min of the stage's groups
-//   Vw  [128][HD*VB/8]             the stage's V rows as stored
-//   Vs, Vm  fp16 [HD/32][128]      V scale / min, channel group major
+//   V   VB = 8: [128][HD*VB/8] the stage's V rows as stored.  VB = 2, 4: per
+//       group [word w][byte b][token pair tp] uint32 = (byte b of word w of
+//       token 2 tp, 0, the same byte of token 2 tp + 1, 0): the PV operand
+//       pairs of one channel, so the matrix operand is one AND of a 16-byte
+//       read (groups padded by 16 words so the stores spread over the banks)
+//   Vs  fp16 [HD/32][128]          V scale, channel group major
+//   Vm  fp16 [HD/32 + 1][128]      V min, channel group major; the extra row
+//                                  holds ones (the sum_t p row of the bias product)
 // ---------------------------------------------------------------------------
 constexpr int kStage = 128;
 
@@ -163,9 +176,12 @@ struct StageLayout {
   static constexpr int off_vw = off_km + 4 * HD * 2;
   static constexpr int vrow_words = HD * VB / 32;
   static constexpr int vrow_bytes = HD * VB / 8;
-  static constexpr int off_vs = off_vw + kStage * vrow_bytes;
+  static constexpr bool vspread = VB != 8;
+  static constexpr int vgrp_words = vrow_words * 64 + 16;   // spread group stride (words)
+  static constexpr int vw_bytes = vspread ? 4 * vgrp_words * 4 : kStage * vrow_bytes;
+  static constexpr int off_vs = off_vw + vw_bytes;
   static constexpr int off_vm = off_vs + (HD / 32) * kStage * 2;
-  static constexpr int bytes = off_vm + (HD / 32) * kStage * 2;
+  static constexpr int bytes = off_vm + (HD / 32 + 1) * kStage * 2;
 };
 
 // One lane's share of a stage's global loads (256 lanes).
@@ -175,11 +191,44 @@ struct StageRegs {
   static constexpr int NK = (KP + kThreads - 1) / kThreads;
   static constexpr int VP = HD * VB;                      // 16-byte V pieces (the stage's rows)
   static constexpr int NV = (VP + kThreads - 1) / kThreads;
+  // spread V (VB = 2, 4): items (token pair, PW-word slice of both rows), slice fastest
+  static constexpr int W = HD * VB / 32;                  // words per V row
+  static constexpr int PW = (W >= 16) ? 4 : 2;
+  static constexpr int NQ = W / PW;                       // slices per row
+  static constexpr int VI = 64 * NQ;                      // items per stage
+  static constexpr int NVI = (VI + kThreads - 1) / kThreads;
+  static constexpr bool spread = VB != 8;
   u4_t k[NK];
-  u4_t v[NV];
+  u4_t v[spread ? 1 : NV];
+  u4_t va[spread ? NVI : 1], vb[spread ? NVI : 1];   // slices of tokens 2 tp and 2 tp + 1
   u2_t km;     // lanes < 2 HD: the 4 group scales (lane < HD) or mins of channel lane % HD
   u2_t vm;     // V scales (lanes < 128) or mins of token lane % 128 (HD = 64: low word only)
 };
+
+// V slice loads of a stage (spread layout): rows 2 tp and 2 tp + 1, clamped to t_last
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void load_vslices(StageRegs<HD, KB, VB>& r, const uint8_t* vseg, int ts,
+                                             int t_last, int tid) {
+  using R = StageRegs<HD, KB, VB>;
+  constexpr int RB = HD * VB / 8;
+#pragma unroll
+  for (int i = 0; i < R::NVI; ++i) {
+    const int q = (tid + kThreads * i) % R::VI;
+    const int tp = q / R::NQ, qw = q - tp * R::NQ;
+    const int ta = min(ts + 2 * tp, t_last), tb = min(ts + 2 * tp + 1, t_last);
+    const uint8_t* pa = vseg + (int64_t)ta * RB + qw * R::PW * 4;
+    const uint8_t* pb = vseg + (int64_t)tb * RB + qw * R::PW * 4;
+    if constexpr (R::PW == 4) {
+      r.va[i] = *reinterpret_cast<const u4_t*>(pa);
+      r.vb[i] = *reinterpret_cast<const u4_t*>(pb);
+    } else {
+      const u2_t a = *reinterpret_cast<const u2_t*>(pa);
+      const u2_t b = *reinterpret_cast<const u2_t*>(pb);
+      r.va[i] = u4_t{a[0], a[1], 0u, 0u};
+      r.vb[i] = u4_t{b[0], b[1], 0u, 0u};
+    }
+  }
+}
 
 struct SegOffsets {
   int64_t kd, km, vd, vm;
@@ -229,7 +278,7 @@ __device__ __forceinline__ void load_stage(StageRegs<HD, KB, VB>& r, const SegDe
   }
   if (tid < 2 * HD) {
     const int c = tid % HD;
-    const uint16_t* m = ((tid < HD) ? s.ks : s.km) + o.km + (int64_t)c * kl.row_groups;
+    const uint16_t* m = pick(tid < HD, s.ks, s.km) + o.km + (int64_t)c * kl.row_groups;
     const int g0 = min(ts / 32, kl.row_groups - 1);
     if (kl.kmeta4) {
       r.km = *reinterpret_cast<const u2_t*>(m + g0);
@@ -240,17 +289,21 @@ __device__ __forceinline__ void load_stage(StageRegs<HD, KB, VB>& r, const SegDe
       r.km = u2_t{x[0] | (x[1] << 16), x[2] | (x[3] << 16)};
     }
   }
-  const int last_piece = (t_last - ts + 1) * (L::vrow_bytes / 16) - 1;
-  const uint8_t* vsrc = s.vd + o.vd + (int64_t)ts * L::vrow_bytes;
+  if constexpr (R::spread) {
+    load_vslices<HD, KB, VB>(r, s.vd + o.vd, ts, t_last, tid);
+  } else {
+    const int last_piece = (t_last - ts + 1) * (L::vrow_bytes / 16) - 1;
+    const uint8_t* vsrc = s.vd + o.vd + (int64_t)ts * L::vrow_bytes;
 #pragma unroll
-  for (int i = 0; i < R::NV; ++i) {
-    const int q = tid + kThreads * i;
-    if (R::VP % kThreads == 0 || q < R::VP)
-      r.v[i] = *reinterpret_cast<const u4_t*>(vsrc + (int64_t)min(q, last_piece) * 16);
+    for (int i = 0; i < R::NV; ++i) {
+      const int q = tid + kThreads * i;
+      if (R::VP % kThreads == 0 || q < R::VP)
+        r.v[i] = *reinterpret_cast<const u4_t*>(vsrc + (int64_t)min(q, last_piece) * 16);
+    }
   }
   {
     const int t = min(ts + (tid & (kStage - 1)), t_last);
-    const uint16_t* m = ((tid < kStage) ? s.vs : s.vm) + o.vm + (int64_t)t * (HD / 32);
+    const uint16_t* m = pick(tid < kStage, s.vs, s.vm) + o.vm + (int64_t)t * (HD / 32);
     if (HD == 128) {
       r.vm = *reinterpret_cast<const u2_t*>(m);
     } else {
@@ -287,19 +340,23 @@ __device__ __forceinline__ void load_stage_fast(StageRegs<HD, KB, VB>& r, const 
     r.k[i] = *reinterpret_cast<const u4_t*>(krows + fo.krow[i] + min(byte0 + kj, kmax));
   }
   {
-    const uint16_t* m = ((tid & (2 * HD - 1)) < HD ? s.ks : s.km) + o.km;
+    const uint16_t* m = pick((tid & (2 * HD - 1)) < HD, s.ks, s.km) + o.km;
     r.km = *reinterpret_cast<const u2_t*>(m + fo.mrow + ts / 32);
   }
-  const int last_piece = (t_last - ts + 1) * (L::vrow_bytes / 16) - 1;
-  const uint8_t* vsrc = s.vd + o.vd + (int64_t)ts * L::vrow_bytes;
+  if constexpr (R::spread) {
+    load_vslices<HD, KB, VB>(r, s.vd + o.vd, ts, t_last, tid);
+  } else {
+    const int last_piece = (t_last - ts + 1) * (L::vrow_bytes / 16) - 1;
+    const uint8_t* vsrc = s.vd + o.vd + (int64_t)ts * L::vrow_bytes;
 #pragma unroll
-  for (int i = 0; i < R::NV; ++i) {
-    const int q = (tid + kThreads * i) & (R::VP - 1);
-    r.v[i] = *reinterpret_cast<const u4_t*>(vsrc + min(q, last_piece) * 16);
+    for (int i = 0; i < R::NV; ++i) {
+      const int q = (tid + kThreads * i) & (R::VP - 1);
+      r.v[i] = *reinterpret_cast<const u4_t*>(vsrc + min(q, last_piece) * 16);
+    }
   }
   {
     const int t = min(ts + (tid & (kStage - 1)), t_last);
-    const uint16_t* m = ((tid < kStage) ? s.vs : s.vm) + o.vm + (int64_t)t * (HD / 32);
+    const uint16_t* m = pick(tid < kStage, s.vs, s.vm) + o.vm + (int64_t)t * (HD / 32);
     if (HD == 128) r.vm = *reinterpret_cast<const u2_t*>(m);
     else r.vm = u2_t{*reinterpret_cast<const uint32_t*>(m), 0u};
   }
@@ -325,11 +382,28 @@ __device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, int 
 #pragma unroll
     for (int g = 0; g < 4; ++g) m[g * HD + c] = (uint16_t)(r.km[g >> 1] >> (16 * (g & 1)));
   }
-  u4_t* vw = reinterpret_cast<u4_t*>(st + L::off_vw);
+  if constexpr (R::spread) {
+    uint32_t* vsp = reinterpret_cast<uint32_t*>(st + L::off_vw);
 #pragma unroll
-  for (int i = 0; i < R::NV; ++i) {
-    const int q = tid + kThreads * i;
-    if (R::VP % kThreads == 0 || q < R::VP) vw[q] = r.v[i];
+    for (int i = 0; i < R::NVI; ++i) {
+      const int q = tid + kThreads * i;
+      if (R::VI % kThreads == 0 || q < R::VI) {
+        const int tp = q / R::NQ, qw = q - tp * R::NQ;
+        uint32_t* dst = vsp + (tp >> 4) * L::vgrp_words + (tp & 15);
+#pragma unroll
+        for (int k = 0; k < R::PW; ++k)
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            dst[((qw * R::PW + k) * 4 + b) * 16] = perm(r.vb[i][k], r.va[i][k], sel_bytes(b));
+      }
+    }
+  } else {
+    u4_t* vw = reinterpret_cast<u4_t*>(st + L::off_vw);
+#pragma unroll
+    for (int i = 0; i < R::NV; ++i) {
+      const int q = tid + kThreads * i;
+      if (R::VP % kThreads == 0 || q < R::VP) vw[q] = r.v[i];
+    }
   }
   {
     uint16_t* m = reinterpret_cast<uint16_t*>(st + ((tid < kStage) ? L::off_vs : L::off_vm));
@@ -474,35 +548,29 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
   }
   // p is rounded to fp16 once; the sum l, P' and the V-min bias all use that
   // rounded value, so the rounding only perturbs the softmax weights.
-  uint32_t p2[4];
-  float psum = 0.f;
+  u4_t p2;
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    p2[m] = pack_h2(p[2 * m], p[2 * m + 1]);
-    psum = dot2(p2[m], kOnes2, psum);
-  }
-  acc.l += psum;
-  // ---- P' = p * sV per channel group, and the V-min bias ----
+  for (int m = 0; m < 4; ++m) p2[m] = pack_h2(p[2 * m], p[2 * m + 1]);
+  // 8 fp16 of channel-group row c of Vs / Vm for this lane's PV tokens
+  auto vmeta8 = [&](const char* base, int c) -> u4_t {
+    if constexpr (KB == 8) {
+      const u2_t x0 = lds_u2(base + (c * kStage + 4 * g4) * 2);
+      const u2_t x1 = lds_u2(base + (c * kStage + 16 + 4 * g4) * 2);
+      return u4_t{x0[0], x0[1], x1[0], x1[1]};
+    } else {
+      return lds_u4(base + (c * kStage + 8 * g4) * 2);
+    }
+  };
+  // ---- V-min bias and sum_t p on the matrix cores: A row c < CG holds the
+  // mins of channel group c, row CG ones (rows above are not used) ----
+  acc.vbl = mfma(vmeta8(vmg, min(r, CG)), p2, acc.vbl);
+  // ---- P' = p * sV per channel group ----
   u4_t pp[CG];
 #pragma unroll
   for (int c = 0; c < CG; ++c) {
-    u4_t sv, mv;
-    if constexpr (KB == 8) {
-      const u2_t s0 = lds_u2(vsg + (c * kStage + 4 * g4) * 2);
-      const u2_t s1 = lds_u2(vsg + (c * kStage + 16 + 4 * g4) * 2);
-      const u2_t m0 = lds_u2(vmg + (c * kStage + 4 * g4) * 2);
-      const u2_t m1 = lds_u2(vmg + (c * kStage + 16 + 4 * g4) * 2);
-      sv = u4_t{s0[0], s0[1], s1[0], s1[1]};
-      mv = u4_t{m0[0], m0[1], m1[0], m1[1]};
-    } else {
-      sv = lds_u4(vsg + (c * kStage + 8 * g4) * 2);
-      mv = lds_u4(vmg + (c * kStage + 8 * g4) * 2);
-    }
+    const u4_t sv = vmeta8(vsg, c);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      pp[c][m] = pkmul(p2[m], sv[m]);
-      acc.vb[c] = dot2(p2[m], mv[m], acc.vb[c]);
-    }
+    for (int m = 0; m < 4; ++m) pp[c][m] = pkmul(p2[m], sv[m]);
   }
   // ---- O^T += codes_V^T * P' : channel block b, row r <-> channel 16 b + r ----
   constexpr int RW = L::vrow_words;
@@ -510,44 +578,28 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
   int tok[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) tok[j] = pv_token<KB>(g4, j);
-  if constexpr (VB == 2) {
-    // a 16-channel block is one word of a V row; 4 blocks per 16-byte read
-    const uint32_t vsel = sel_bytes(r >> 2);
-    const uint32_t vmask = 0x00030003u << (2 * (r & 3));
+  if constexpr (L::vspread) {
+    // spread rows: word w, byte b, token pair; row r of block bb is channel 16 bb + r
+    const uint32_t* vsp = reinterpret_cast<const uint32_t*>(st + L::off_vw) + grp * L::vgrp_words;
+    const int byte = (VB == 2) ? (r >> 2) : ((r >> 1) & 3);
+    const uint32_t vmask = (VB == 2) ? (0x00030003u << (2 * (r & 3))) : (0x000F000Fu << (4 * (r & 1)));
 #pragma unroll
-    for (int k = 0; k < NB / 4; ++k) {
-      u4_t w[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) w[j] = lds_u4(vw + (tok[j] * RW + 4 * k) * 4);
-#pragma unroll
-      for (int bb = 0; bb < 4; ++bb) {
-        u4_t a;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) a[m] = perm(w[2 * m + 1][bb], w[2 * m][bb], vsel) & vmask;
-        acc.o[4 * k + bb] = mfma(a, pp[(4 * k + bb) >> 1], acc.o[4 * k + bb]);
+    for (int bb = 0; bb < NB; ++bb) {
+      const int w = (VB == 2) ? bb : (2 * bb + (r >> 3));
+      const uint32_t* src = vsp + (w * 4 + byte) * 16;
+      u4_t x;
+      if constexpr (KB == 8) {
+        // PV slots (2m, 2m + 1) hold the token pair 8 (m >> 1) + 2 g4 + (m & 1)
+        const u2_t x0 = *reinterpret_cast<const u2_t*>(src + 2 * g4);
+        const u2_t x1 = *reinterpret_cast<const u2_t*>(src + 8 + 2 * g4);
+        x = u4_t{x0[0], x0[1], x1[0], x1[1]};
+      } else {
+        x = *reinterpret_cast<const u4_t*>(src + 4 * g4);
       }
-    }
-  } else if constexpr (VB == 4) {
-    // block b spans two words; rows r >= 8 take the second one
-    const uint32_t vsel = sel_bytes((r >> 1) & 3);
-    const uint32_t vmask = 0x000F000Fu << (4 * (r & 1));
-    const bool hi = (r >> 3) != 0;
+      u4_t a;
 #pragma unroll
-    for (int k = 0; k < NB / 2; ++k) {
-      u4_t w[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) w[j] = lds_u4(vw + (tok[j] * RW + 4 * k) * 4);
-#pragma unroll
-      for (int bb = 0; bb < 2; ++bb) {
-        u4_t a;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const uint32_t wa = hi ? w[2 * m][2 * bb + 1] : w[2 * m][2 * bb];
-          const uint32_t wb = hi ? w[2 * m + 1][2 * bb + 1] : w[2 * m + 1][2 * bb];
-          a[m] = perm(wb, wa, vsel) & vmask;
-        }
-        acc.o[2 * k + bb] = mfma(a, pp[(2 * k + bb) >> 1], acc.o[2 * k + bb]);
-      }
+      for (int m = 0; m < 4; ++m) a[m] = x[m] & vmask;
+      acc.o[bb] = mfma(a, pp[bb >> 1], acc.o[bb]);
     }
   } else {
     const uint32_t vsel = sel_bytes(r & 3);
@@ -693,6 +745,15 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
   };
   char* buf0 = lds;
   char* buf1 = lds + stage_bytes;
+  {
+    // the ones row of both buffers' V-min block (never overwritten by the stages)
+    using L = StageLayout<HD, KB, VB>;
+    constexpr int CG = HD / 32;
+    for (int t = tid; t < kStage; t += kThreads) {
+      reinterpret_cast<uint16_t*>(buf0 + L::off_vm)[CG * kStage + t] = 0x3C00;
+      reinterpret_cast<uint16_t*>(buf1 + L::off_vm)[CG * kStage + t] = 0x3C00;
+    }
+  }
   R ra, rb;
   int i = 0;
   if constexpr (DEPTH == 2) {
@@ -821,8 +882,7 @@ decode_mfma_kernel(const DecodeParams p) {
   WaveAcc<HD> acc;
 #pragma unroll
   for (int i = 0; i < NB; ++i) acc.o[i] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < HD / 32; ++i) acc.vb[i] = 0.f;
+  acc.vbl = f4_t{0.f, 0.f, 0.f, 0.f};
   acc.m = -INFINITY;
   acc.mx = -INFINITY;
   acc.l = 0.f;
@@ -857,18 +917,18 @@ decode_mfma_kernel(const DecodeParams p) {
     const float alpha = __builtin_amdgcn_exp2f(acc.m - acc.mx);
     acc.m = acc.mx;
     acc.l *= alpha;
+    acc.vbl *= alpha;
 #pragma unroll
     for (int i = 0; i < NB; ++i) acc.o[i] *= alpha;
-#pragma unroll
-    for (int i = 0; i < HD / 32; ++i) acc.vb[i] *= alpha;
   }
   // ---- wave results -> LDS, merge the 4 waves ----
   __syncthreads();
   float* mo = reinterpret_cast<float*>(lds);               // [4][16][HD]
   float* mm = mo + kWaves * 16 * HD;                        // [4][16]
   float* ml = mm + kWaves * 16;                             // [4][16]
-  const float l_full = xsum4(acc.l);
+  float l_full;
   if (s.kind == PK_SEG_FP16) {
+    l_full = xsum4(acc.l);
     // result row r of block bb is channel NB r + bb: 8 consecutive channels per (g4, e)
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -877,9 +937,13 @@ decode_mfma_kernel(const DecodeParams p) {
         *reinterpret_cast<f4_t*>(mo + (wave * 16 + n) * HD + NB * (4 * g4 + e) + bb) =
             f4_t{acc.o[bb][e], acc.o[bb + 1][e], acc.o[bb + 2][e], acc.o[bb + 3][e]};
   } else {
-    float vbf[HD / 32];
+    // rows c < HD/32 of the bias product sit in lane group 0, row HD/32 in lane
+    // group HD/128 (register (HD/32) % 4)
+    constexpr int CG = HD / 32;
+    float vbf[CG];
 #pragma unroll
-    for (int c = 0; c < HD / 32; ++c) vbf[c] = xsum4(acc.vb[c]);
+    for (int c = 0; c < CG; ++c) vbf[c] = __shfl(acc.vbl[c], n);
+    l_full = __shfl(acc.vbl[CG % 4], 16 * (CG / 4) + n);
     // V code position factor of result row 4 g4 + e
     const int vb_bits = s.vbits;
     f4_t f;
