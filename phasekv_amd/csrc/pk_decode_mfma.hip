@@ -702,10 +702,11 @@ __device__ __forceinline__ void fp16_group(const uint16_t* kbase, const uint16_t
 // ---------------------------------------------------------------------------
 // one 32-token group of stage i (wave w computes group w of each stage)
 template <int HD, int KB, int VB>
-__device__ __forceinline__ void stage_group(const char* st, int i, int t_begin, int t_end,
-                                            int wave, int lane, const u4_t (&qb)[HD / 32],
-                                            WaveAcc<HD>& acc, float sl2) {
-  const int t0 = t_begin + i * kStage + kTile * wave;
+__device__ __forceinline__ void stage_group(const char* st, int i, int t_first, int t_stride,
+                                            int t_end, int wave, int lane,
+                                            const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
+                                            float sl2) {
+  const int t0 = t_first + i * t_stride + kTile * wave;
   if (t0 < t_end) {
     const int nvalid = min(kTile, t_end - t0);
     if (nvalid == kTile) kivi_group<HD, KB, VB, true>(nvalid, st, wave, qb, acc, sl2, lane);
@@ -722,14 +723,13 @@ __device__ __forceinline__ void stage_group(const char* st, int i, int t_begin, 
 // only for the stage it stores.  Otherwise the general loads of load_stage.
 template <int HD, int KB, int VB, bool FAST>
 __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o,
-                                            const KivLoad& kl, int t_begin, int t_end, int wave,
-                                            int lane, int tid, char* lds, int stage_bytes,
-                                            const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
-                                            float sl2) {
+                                            const KivLoad& kl, int t_first, int t_stride, int nst,
+                                            int t_end, int wave, int lane, int tid, char* lds,
+                                            int stage_bytes, const u4_t (&qb)[HD / 32],
+                                            WaveAcc<HD>& acc, float sl2) {
   using R = StageRegs<HD, KB, VB>;
   constexpr int DEPTH = (KB + VB <= 4) ? 2 : 1;
   const int t_last = t_end - 1;
-  const int nst = (t_end - t_begin + kStage - 1) / kStage;
   FastOffsets<HD, KB, VB> fo;
   if constexpr (FAST) {
 #pragma unroll
@@ -740,8 +740,8 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
     fo.mrow = (uint32_t)((tid & (HD - 1)) * kl.row_groups);
   }
   auto load = [&](R& r, int st) {
-    if constexpr (FAST) load_stage_fast<HD, KB, VB>(r, s, o, kl, fo, t_begin + st * kStage, t_last, tid);
-    else load_stage<HD, KB, VB>(r, s, o, kl, t_begin + st * kStage, t_last, tid);
+    if constexpr (FAST) load_stage_fast<HD, KB, VB>(r, s, o, kl, fo, t_first + st * t_stride, t_last, tid);
+    else load_stage<HD, KB, VB>(r, s, o, kl, t_first + st * t_stride, t_last, tid);
   };
   char* buf0 = lds;
   char* buf1 = lds + stage_bytes;
@@ -766,18 +766,19 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
     __syncthreads();
     // steady state: stages i + 1 and i + 2 in flight, i + 3 and i + 4 loaded here
     for (; i + 4 < nst; i += 2) {
-      stage_group<HD, KB, VB>(buf0, i, t_begin, t_end, wave, lane, qb, acc, sl2);
+      stage_group<HD, KB, VB>(buf0, i, t_first, t_stride, t_end, wave, lane, qb, acc, sl2);
       store_stage<HD, KB, VB>(rb, tid, buf1);
       load(rb, i + 3);
       __syncthreads();
-      stage_group<HD, KB, VB>(buf1, i + 1, t_begin, t_end, wave, lane, qb, acc, sl2);
+      stage_group<HD, KB, VB>(buf1, i + 1, t_first, t_stride, t_end, wave, lane, qb, acc, sl2);
       store_stage<HD, KB, VB>(ra, tid, buf0);
       load(ra, i + 4);
       __syncthreads();
     }
     // tail: at most four stages left, none loaded beyond nst
     for (; i < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_begin, t_end, wave, lane, qb, acc, sl2);
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, wave, lane, qb,
+                              acc, sl2);
       if (i + 1 < nst) {
         if (i & 1) {
           store_stage<HD, KB, VB>(ra, tid, buf0);
@@ -795,13 +796,15 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
     if (nst > 1) load(ra, 1);
     __syncthreads();
     for (; i + 2 < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_begin, t_end, wave, lane, qb, acc, sl2);
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, wave, lane, qb,
+                              acc, sl2);
       store_stage<HD, KB, VB>(ra, tid, (i & 1) ? buf0 : buf1);
       load(ra, i + 2);
       __syncthreads();
     }
     for (; i < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_begin, t_end, wave, lane, qb, acc, sl2);
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, wave, lane, qb,
+                              acc, sl2);
       if (i + 1 < nst) {
         store_stage<HD, KB, VB>(ra, tid, (i & 1) ? buf0 : buf1);
         __syncthreads();
@@ -810,28 +813,30 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
   }
 }
 
+// Stages of the chunk: t_first + i t_stride (i < nst), tokens below t_end.
 template <int HD, int KB, int VB>
-__device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_begin,
-                                           int t_end, int wave, int lane, int tid, char* lds,
-                                           int stage_bytes, const u4_t (&qb)[HD / 32],
-                                           WaveAcc<HD>& acc, float sl2) {
+__device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_first,
+                                           int t_stride, int nst, int t_end, int wave, int lane,
+                                           int tid, char* lds, int stage_bytes,
+                                           const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
+                                           float sl2) {
   KivLoad kl;
   kl.row_bytes = ((int64_t)s.length * KB + 7) / 8;
   kl.row_groups = (s.length + s.kgs - 1) / s.kgs;
-  const int64_t byte_begin = (int64_t)t_begin * KB / 8;
+  const int64_t byte_begin = (int64_t)t_first * KB / 8;
   const uintptr_t kaddr = reinterpret_cast<uintptr_t>(s.kd + o.kd);
   if (kl.row_bytes % 16 == 0 && byte_begin % 16 == 0 && kaddr % 16 == 0) kl.kmode = 16;
   else if (kl.row_bytes % 4 == 0 && byte_begin % 4 == 0 && kaddr % 4 == 0) kl.kmode = 4;
   else kl.kmode = 1;
-  kl.kmeta4 = (kl.row_groups % 4 == 0) && (t_begin % kStage == 0) &&
+  kl.kmeta4 = (kl.row_groups % 4 == 0) && (t_first % kStage == 0) && (t_stride % kStage == 0) &&
               (reinterpret_cast<uintptr_t>(s.ks + o.km) % 8 == 0) &&
               (reinterpret_cast<uintptr_t>(s.km + o.km) % 8 == 0);
   if (kl.kmode == 16 && kl.kmeta4 && kl.row_bytes < ((int64_t)1 << 31) / HD)
-    kivi_stages<HD, KB, VB, true>(s, o, kl, t_begin, t_end, wave, lane, tid, lds, stage_bytes, qb,
-                                  acc, sl2);
+    kivi_stages<HD, KB, VB, true>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
+                                  stage_bytes, qb, acc, sl2);
   else
-    kivi_stages<HD, KB, VB, false>(s, o, kl, t_begin, t_end, wave, lane, tid, lds, stage_bytes,
-                                   qb, acc, sl2);
+    kivi_stages<HD, KB, VB, false>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
+                                   stage_bytes, qb, acc, sl2);
 }
 
 // Two workgroups (8 waves) per CU: the register budget is capped so a second
@@ -898,13 +903,16 @@ decode_mfma_kernel(const DecodeParams p) {
     o.km = b * s.km_bs + kvh * s.km_hs;
     o.vd = b * s.vd_bs + kvh * s.vd_hs;
     o.vm = b * s.vm_bs + kvh * s.vm_hs;
+    // the chunk's 128-token stages (none when a ragged row ends before it)
+    const int kt_first = t_begin, kt_stride = kStage, kt_end = t_end;
+    const int knst = (kt_end > kt_first) ? (kt_end - kt_first - 1) / kt_stride + 1 : 0;
     // only the bit widths up to MAXB are compiled into this kernel variant,
     // which keeps the register budget of the common 2/4-bit cases low
 #define PK_KIVI_CASE(KB_, VB_)                                                                 \
   if constexpr (KB_ <= MAXB && VB_ <= MAXB) {                                                  \
-    if (s.kbits == KB_ && s.vbits == VB_)                                                      \
-      kivi_chunk<HD, KB_, VB_>(s, o, t_begin, t_end, wave, lane, tid, lds, p.stage_lds, qb, acc, \
-                               sl2);                                                           \
+    if (knst > 0 && s.kbits == KB_ && s.vbits == VB_)                                          \
+      kivi_chunk<HD, KB_, VB_>(s, o, kt_first, kt_stride, knst, kt_end, wave, lane, tid, lds,  \
+                               p.stage_lds, qb, acc, sl2);                                     \
   }
     PK_KIVI_CASE(2, 2) PK_KIVI_CASE(2, 4) PK_KIVI_CASE(2, 8)
     PK_KIVI_CASE(4, 2) PK_KIVI_CASE(4, 4) PK_KIVI_CASE(4, 8)
