@@ -73,11 +73,14 @@ int pk_unpack_low_bits(const uint8_t* packed, int64_t rows, int64_t packed_len, 
  * resolved by the caller to gs = min(group_size, len) (or len).  Outputs are
  * contiguous in the moved layout: out_packed [rows, ceil(len/vpb)],
  * out_scale/out_mins fp16 [rows, ceil(len/gs)], rows = prod(shape) / len in
- * the original order of the remaining dims.  Bit-exact with the reference. */
+ * the original order of the remaining dims (meta_layout PK_META_CHANNEL_MAJOR),
+ * or, for axis == ndim - 2 only, that array's last two dims transposed
+ * (PK_META_GROUP_MAJOR: [rows / D, ceil(len/gs), D], D = shape[ndim - 1]).
+ * Bit-exact with the reference. */
 int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_t* shape,
                      const int64_t* strides, int axis, int bits, int group_size,
                      uint8_t* out_packed, uint16_t* out_scale, uint16_t* out_mins,
-                     void* stream);
+                     int meta_layout, void* stream);
 
 /* unpack_dequantize (packing.py:158-175): inverse of pk_quantize_pack.  Writes
  * fp16 out contiguous in the ORIGINAL layout orig_shape (ndim <= 8), with
@@ -92,6 +95,14 @@ int pk_unpack_dequantize(const uint8_t* packed, const uint16_t* scale, const uin
  * dims of packed / meta buffers are contiguous.  For PK_SEG_FP16 the K/V data
  * pointers are fp16 and k_meta / v_meta strides are unused; tok_stride is the
  * element stride between tokens (hd is contiguous). */
+/* Storage of a KIVI K segment's scale / min (logical shape [..., head_dim, groups]):
+ * channel major is the reference's contiguous layout; group major stores the
+ * transpose, [..., groups, head_dim] contiguous, so that the scales of a few
+ * consecutive groups of every channel are one contiguous run.  pk_quantize_pack
+ * writes either; the decode kernels read either. */
+#define PK_META_CHANNEL_MAJOR 0
+#define PK_META_GROUP_MAJOR 1
+
 typedef struct pk_segment {
   int32_t kind;            /* PK_SEG_* */
   int32_t length;          /* tokens in the segment (max over the batch) */
@@ -101,6 +112,8 @@ typedef struct pk_segment {
   int32_t split_len;       /* tokens per split; with splits > 0 exactly `splits` splits of
                               split_len tokens are launched (trailing ones may be empty, like
                               attention_triton.py:227-240); 0 = split_len = ceil(len / splits) */
+  int32_t k_meta_layout;   /* KIVI K scale/min storage: PK_META_CHANNEL_MAJOR or PK_META_GROUP_MAJOR */
+  int32_t reserved;        /* 0 */
   const int32_t* seq_lens; /* device [batch] valid tokens per row, or NULL (= length) */
   const void* k_data; const uint16_t* k_scale; const uint16_t* k_mins;
   const void* v_data; const uint16_t* v_scale; const uint16_t* v_mins;

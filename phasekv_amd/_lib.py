@@ -29,6 +29,9 @@ PK_SEG_FP16 = 2
 PK_MAX_SEGMENTS_PER_LAUNCH = 8
 PK_FLAG_GENERIC_KERNEL = 1
 
+PK_META_CHANNEL_MAJOR = 0
+PK_META_GROUP_MAJOR = 1
+
 _c_i32 = ctypes.c_int32
 _c_i64 = ctypes.c_int64
 _c_vp = ctypes.c_void_p
@@ -40,6 +43,7 @@ class PkSegment(ctypes.Structure):
     _fields_ = [
         ("kind", _c_i32), ("length", _c_i32), ("k_bits", _c_i32), ("v_bits", _c_i32),
         ("k_group", _c_i32), ("v_group", _c_i32), ("splits", _c_i32), ("split_len", _c_i32),
+        ("k_meta_layout", _c_i32), ("reserved", _c_i32),
         ("seq_lens", _c_vp),
         ("k_data", _c_vp), ("k_scale", _c_vp), ("k_mins", _c_vp),
         ("v_data", _c_vp), ("v_scale", _c_vp), ("v_mins", _c_vp),
@@ -76,7 +80,7 @@ _SIGNATURES = {
     "pk_quantize_pack": (ctypes.c_int, [_c_vp, ctypes.c_int, ctypes.c_int,
                                         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64),
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                        _c_vp, _c_vp, _c_vp, _c_vp]),
+                                        _c_vp, _c_vp, _c_vp, ctypes.c_int, _c_vp]),
     "pk_unpack_dequantize": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, ctypes.c_int,
                                             ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int, _c_i64, _c_vp, _c_vp]),

@@ -35,7 +35,7 @@ __device__ __forceinline__ float kivi_k_elem(const SegDev& s, int64_t kd_off, in
   const int64_t row_groups = (s.length + s.kgs - 1) / s.kgs;
   const uint32_t byte = s.kd[kd_off + d * row_bytes + tok / vpb];
   const uint32_t code = (byte >> ((tok % vpb) * s.kbits)) & ((1u << s.kbits) - 1u);
-  const int64_t g = d * row_groups + tok / s.kgs;
+  const int64_t g = s.kmeta_gm ? (int64_t)(tok / s.kgs) * s.hd_meta + d : d * row_groups + tok / s.kgs;
   return static_cast<float>(code) * pk_h2f(s.ks[km_off + g]) + pk_h2f(s.km[km_off + g]);
 }
 
@@ -318,6 +318,9 @@ static int validate_problem(const pk_decode_problem* p) {
       return fail("segment " + std::to_string(i) + ": null scale/min");
     if (s.kind == PK_SEG_KIVI && s.k_group > s.length)
       return fail("K group size exceeds the segment length");
+    if (s.k_meta_layout != PK_META_CHANNEL_MAJOR &&
+        (s.k_meta_layout != PK_META_GROUP_MAJOR || s.kind != PK_SEG_KIVI))
+      return fail("k_meta_layout must be channel major, or group major for a KIVI segment");
     if (s.v_group > hd) return fail("V group size exceeds head_dim");
     if (s.kind == PK_SEG_TOKEN && s.k_group > hd) return fail("K group size exceeds head_dim");
   }
@@ -461,6 +464,7 @@ static void fill_segment(SegDev& d, const pk_segment& s) {
   d.vd_bs = s.v_data_bstride; d.vd_hs = s.v_data_hstride;
   d.vm_bs = s.v_meta_bstride; d.vm_hs = s.v_meta_hstride;
   d.tok_stride = s.tok_stride;
+  d.kmeta_gm = s.kind == PK_SEG_KIVI && s.k_meta_layout == PK_META_GROUP_MAJOR;
 }
 
 static size_t generic_lds_bytes(const Plan& pl, int hd) {
@@ -494,6 +498,7 @@ static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
     for (int i = 0; i < n; ++i) {
       SegDev& d = dp.seg[i];
       fill_segment(d, p->segments[first + i]);
+      d.hd_meta = p->head_dim;
       d.chunk_len = pl.chunk_len[first + i];
       d.n_chunks = pl.n_chunks[first + i];
       d.gbegin = pl.gbegin[first + i];

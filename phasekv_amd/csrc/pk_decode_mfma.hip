@@ -239,8 +239,40 @@ struct KivLoad {
   int64_t row_bytes;   // bytes of one channel's K codes
   int row_groups;      // K groups per channel
   int kmode;           // 16, 4 or 1
-  bool kmeta4;         // the 4 group scales of a stage are one aligned 8-byte load
+  bool kmeta4;         // channel major: the 4 group scales of a stage are one aligned 8-byte load
+  bool kmeta_gm;       // group major: a stage's scales are [4][HD] contiguous (8-byte loads)
+  bool gm_elems;       // group major but not 8-byte aligned: per-element loads
 };
+
+// K scale/min of a stage: in lane order.  Channel major: lane (tensor, channel)
+// holds the stage's 4 groups of its channel.  Group major: lane (tensor, group,
+// channel quad) holds 4 channels of one group, stored as read (no transpose).
+template <int HD>
+__device__ __forceinline__ u2_t load_kmeta(const SegDev& s, const SegOffsets& o, const KivLoad& kl,
+                                           int ts, int tid) {
+  const int g0 = min(ts / 32, kl.row_groups - 1);
+  if (kl.kmeta_gm) {
+    const int q = tid & (2 * HD - 1);
+    const int g = min(g0 + (q & (HD - 1)) / (HD / 4), kl.row_groups - 1);
+    const int c4 = q & (HD / 4 - 1);
+    const uint16_t* m = pick(q < HD, s.ks, s.km) + o.km + (int64_t)g * HD + 4 * c4;
+    return *reinterpret_cast<const u2_t*>(m);
+  }
+  const int c = tid % HD;
+  const uint16_t* base = pick((tid & (2 * HD - 1)) < HD, s.ks, s.km) + o.km;
+  if (kl.gm_elems) {
+    uint32_t x[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) x[g] = base[(int64_t)min(g0 + g, kl.row_groups - 1) * HD + c];
+    return u2_t{x[0] | (x[1] << 16), x[2] | (x[3] << 16)};
+  }
+  const uint16_t* m = base + (int64_t)c * kl.row_groups;
+  if (kl.kmeta4) return *reinterpret_cast<const u2_t*>(m + g0);
+  uint32_t x[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) x[g] = m[min(g0 + g, kl.row_groups - 1)];
+  return u2_t{x[0] | (x[1] << 16), x[2] | (x[3] << 16)};
+}
 
 // Loads of the stage starting at token ts (ts - segment start is a multiple of
 // 32).  Addresses stay inside the segment: K pieces past a row's end are not
@@ -276,19 +308,7 @@ __device__ __forceinline__ void load_stage(StageRegs<HD, KB, VB>& r, const SegDe
       r.k[i] = v;
     }
   }
-  if (tid < 2 * HD) {
-    const int c = tid % HD;
-    const uint16_t* m = pick(tid < HD, s.ks, s.km) + o.km + (int64_t)c * kl.row_groups;
-    const int g0 = min(ts / 32, kl.row_groups - 1);
-    if (kl.kmeta4) {
-      r.km = *reinterpret_cast<const u2_t*>(m + g0);
-    } else {
-      uint32_t x[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) x[g] = m[min(g0 + g, kl.row_groups - 1)];
-      r.km = u2_t{x[0] | (x[1] << 16), x[2] | (x[3] << 16)};
-    }
-  }
+  if (tid < 2 * HD) r.km = load_kmeta<HD>(s, o, kl, ts, tid);
   if constexpr (R::spread) {
     load_vslices<HD, KB, VB>(r, s.vd + o.vd, ts, t_last, tid);
   } else {
@@ -316,7 +336,8 @@ __device__ __forceinline__ void load_stage(StageRegs<HD, KB, VB>& r, const SegDe
 template <int HD, int KB, int VB>
 struct FastOffsets {
   uint32_t krow[StageRegs<HD, KB, VB>::NK];   // channel row start of each K piece
-  uint32_t mrow;                             // K metadata: channel row start (elements)
+  uint32_t mrow;                             // K metadata: lane offset (elements)
+  uint32_t mstep;                            // K metadata: elements per group (1 or HD)
 };
 
 // Stage loads for segments whose K rows are 16-byte aligned and hold a
@@ -340,8 +361,11 @@ __device__ __forceinline__ void load_stage_fast(StageRegs<HD, KB, VB>& r, const 
     r.k[i] = *reinterpret_cast<const u4_t*>(krows + fo.krow[i] + min(byte0 + kj, kmax));
   }
   {
-    const uint16_t* m = pick((tid & (2 * HD - 1)) < HD, s.ks, s.km) + o.km;
-    r.km = *reinterpret_cast<const u2_t*>(m + fo.mrow + ts / 32);
+    // both layouts are one aligned 8-byte load per lane; fo.mrow / fo.mstep
+    // hold the layout's lane offset and per-group step
+    const int q = tid & (2 * HD - 1);
+    const uint16_t* m = pick(q < HD, s.ks, s.km) + o.km;
+    r.km = *reinterpret_cast<const u2_t*>(m + fo.mrow + (ts / 32) * fo.mstep);
   }
   if constexpr (R::spread) {
     load_vslices<HD, KB, VB>(r, s.vd + o.vd, ts, t_last, tid);
@@ -363,7 +387,8 @@ __device__ __forceinline__ void load_stage_fast(StageRegs<HD, KB, VB>& r, const 
 }
 
 template <int HD, int KB, int VB>
-__device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, int tid, char* st) {
+__device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, bool kmeta_gm, int tid,
+                                            char* st) {
   using L = StageLayout<HD, KB, VB>;
   using R = StageRegs<HD, KB, VB>;
   uint32_t* kw = reinterpret_cast<uint32_t*>(st);
@@ -378,9 +403,15 @@ __device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, int 
   }
   if (tid < 2 * HD) {
     uint16_t* m = reinterpret_cast<uint16_t*>(st + ((tid < HD) ? L::off_ks : L::off_km));
-    const int c = tid % HD;
+    if (kmeta_gm) {
+      // lane (tensor, group, channel quad): already [group][channel]
+      const int q = tid & (HD - 1);
+      *reinterpret_cast<u2_t*>(m + (q / (HD / 4)) * HD + 4 * (q & (HD / 4 - 1))) = r.km;
+    } else {
+      const int c = tid % HD;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) m[g * HD + c] = (uint16_t)(r.km[g >> 1] >> (16 * (g & 1)));
+      for (int g = 0; g < 4; ++g) m[g * HD + c] = (uint16_t)(r.km[g >> 1] >> (16 * (g & 1)));
+    }
   }
   if constexpr (R::spread) {
     uint32_t* vsp = reinterpret_cast<uint32_t*>(st + L::off_vw);
@@ -737,7 +768,14 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
       const int q = (tid + kThreads * i) & (R::KP - 1);
       fo.krow[i] = (uint32_t)((q / KB) * kl.row_bytes);
     }
-    fo.mrow = (uint32_t)((tid & (HD - 1)) * kl.row_groups);
+    if (kl.kmeta_gm) {
+      const int q = tid & (HD - 1);
+      fo.mrow = (uint32_t)((q / (HD / 4)) * HD + 4 * (q & (HD / 4 - 1)));
+      fo.mstep = HD;
+    } else {
+      fo.mrow = (uint32_t)((tid & (HD - 1)) * kl.row_groups);
+      fo.mstep = 1;
+    }
   }
   auto load = [&](R& r, int st) {
     if constexpr (FAST) load_stage_fast<HD, KB, VB>(r, s, o, kl, fo, t_first + st * t_stride, t_last, tid);
@@ -760,18 +798,18 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
     // stage 0 goes out alone: every workgroup starts at once, and its first
     // stage should not queue behind everybody's next ones
     load(ra, 0);
-    store_stage<HD, KB, VB>(ra, tid, buf0);
+    store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, buf0);
     if (nst > 1) load(rb, 1);
     if (nst > 2) load(ra, 2);
     __syncthreads();
     // steady state: stages i + 1 and i + 2 in flight, i + 3 and i + 4 loaded here
     for (; i + 4 < nst; i += 2) {
       stage_group<HD, KB, VB>(buf0, i, t_first, t_stride, t_end, wave, lane, qb, acc, sl2);
-      store_stage<HD, KB, VB>(rb, tid, buf1);
+      store_stage<HD, KB, VB>(rb, kl.kmeta_gm, tid, buf1);
       load(rb, i + 3);
       __syncthreads();
       stage_group<HD, KB, VB>(buf1, i + 1, t_first, t_stride, t_end, wave, lane, qb, acc, sl2);
-      store_stage<HD, KB, VB>(ra, tid, buf0);
+      store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, buf0);
       load(ra, i + 4);
       __syncthreads();
     }
@@ -781,10 +819,10 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
                               acc, sl2);
       if (i + 1 < nst) {
         if (i & 1) {
-          store_stage<HD, KB, VB>(ra, tid, buf0);
+          store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, buf0);
           if (i + 3 < nst) load(ra, i + 3);
         } else {
-          store_stage<HD, KB, VB>(rb, tid, buf1);
+          store_stage<HD, KB, VB>(rb, kl.kmeta_gm, tid, buf1);
           if (i + 3 < nst) load(rb, i + 3);
         }
         __syncthreads();
@@ -792,13 +830,13 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
     }
   } else {
     load(ra, 0);
-    store_stage<HD, KB, VB>(ra, tid, buf0);
+    store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, buf0);
     if (nst > 1) load(ra, 1);
     __syncthreads();
     for (; i + 2 < nst; ++i) {
       stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, wave, lane, qb,
                               acc, sl2);
-      store_stage<HD, KB, VB>(ra, tid, (i & 1) ? buf0 : buf1);
+      store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, (i & 1) ? buf0 : buf1);
       load(ra, i + 2);
       __syncthreads();
     }
@@ -806,7 +844,7 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
       stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, wave, lane, qb,
                               acc, sl2);
       if (i + 1 < nst) {
-        store_stage<HD, KB, VB>(ra, tid, (i & 1) ? buf0 : buf1);
+        store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, (i & 1) ? buf0 : buf1);
         __syncthreads();
       }
     }
@@ -828,10 +866,16 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
   if (kl.row_bytes % 16 == 0 && byte_begin % 16 == 0 && kaddr % 16 == 0) kl.kmode = 16;
   else if (kl.row_bytes % 4 == 0 && byte_begin % 4 == 0 && kaddr % 4 == 0) kl.kmode = 4;
   else kl.kmode = 1;
-  kl.kmeta4 = (kl.row_groups % 4 == 0) && (t_first % kStage == 0) && (t_stride % kStage == 0) &&
-              (reinterpret_cast<uintptr_t>(s.ks + o.km) % 8 == 0) &&
-              (reinterpret_cast<uintptr_t>(s.km + o.km) % 8 == 0);
-  if (kl.kmode == 16 && kl.kmeta4 && kl.row_bytes < ((int64_t)1 << 31) / HD)
+  const bool meta8 = (reinterpret_cast<uintptr_t>(s.ks + o.km) % 8 == 0) &&
+                     (reinterpret_cast<uintptr_t>(s.km + o.km) % 8 == 0);
+  kl.kmeta_gm = s.kmeta_gm && meta8;
+  kl.gm_elems = s.kmeta_gm && !meta8;
+  kl.kmeta4 = !s.kmeta_gm && (kl.row_groups % 4 == 0) && (t_first % kStage == 0) &&
+              (t_stride % kStage == 0) && meta8;
+  // the fast loads take the stage's 4 groups unclamped: whole 4-group stages only
+  const bool gm_fast = kl.kmeta_gm && (kl.row_groups % 4 == 0) && (t_first % kStage == 0) &&
+                       (t_stride % kStage == 0);
+  if (kl.kmode == 16 && (kl.kmeta4 || gm_fast) && kl.row_bytes < ((int64_t)1 << 31) / HD)
     kivi_stages<HD, KB, VB, true>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
                                   stage_bytes, qb, acc, sl2);
   else

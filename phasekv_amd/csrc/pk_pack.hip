@@ -73,6 +73,8 @@ struct QuantParams {
   int64_t nbytes;
   int64_t rows;
   int rows_fastest;               // thread index -> (row fastest) or (group fastest)
+  int meta_gm;                    // scale/mins group major over the last dim (axis == ndim - 2)
+  int64_t meta_d;                 // that last dim
   uint8_t* packed;
   uint16_t* scale;
   uint16_t* mins;
@@ -87,6 +89,14 @@ __device__ __forceinline__ int64_t row_offset(const QuantParams& p, int64_t r) {
     off += idx * p.pre_stride[d];
   }
   return off;
+}
+
+// Element of scale / mins for (row, group): channel major [rows][ngroups], or
+// group major [rows / D][ngroups][D] (row = outer * D + channel).
+__device__ __forceinline__ int64_t meta_index(const QuantParams& p, int64_t r, int64_t g) {
+  if (!p.meta_gm) return r * p.ngroups + g;
+  const int64_t o = r / p.meta_d;
+  return (o * p.ngroups + g) * p.meta_d + (r - o * p.meta_d);
 }
 
 __device__ __forceinline__ float load_x(const QuantParams& p, int64_t off) {
@@ -142,8 +152,8 @@ quantize_groups_kernel(QuantParams p) {
     else { r = i / p.ngroups; g = i - r * p.ngroups; }
     const int64_t off = row_offset(p, r);
     const GroupStats s = group_stats(p, off, g);
-    p.scale[r * p.ngroups + g] = pk_f2h(s.scale);
-    p.mins[r * p.ngroups + g] = pk_f2h(s.mn);
+    p.scale[meta_index(p, r, g)] = pk_f2h(s.scale);
+    p.mins[meta_index(p, r, g)] = pk_f2h(s.mn);
     const int64_t begin = g * p.gs;
     const int64_t end = min(begin + p.gs, p.len);
     uint8_t* dst = p.packed + r * p.nbytes;
@@ -231,7 +241,7 @@ template <int BITS>
 __global__ void __launch_bounds__(kThreads)
 quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t len, int64_t D,
                         int64_t ngroups, int64_t nbytes, uint8_t* __restrict__ packed,
-                        uint16_t* __restrict__ scale, uint16_t* __restrict__ mins) {
+                        uint16_t* __restrict__ scale, uint16_t* __restrict__ mins, int meta_gm) {
   const int64_t pairs = D / 2;
   const int64_t total = outer * ngroups * pairs;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -252,8 +262,9 @@ quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t l
       const float (&v)[32] = k ? b : a;
       const GroupStats st = stats32(v, BITS);
       const int64_t row = o * D + 2 * cp + k;
-      scale[row * ngroups + g] = pk_f2h(st.scale);
-      mins[row * ngroups + g] = pk_f2h(st.mn);
+      const int64_t mi = meta_gm ? (o * ngroups + g) * D + 2 * cp + k : row * ngroups + g;
+      scale[mi] = pk_f2h(st.scale);
+      mins[mi] = pk_f2h(st.mn);
       uint32_t w[BITS];
       pack32<BITS>(v, st, w);
       uint32_t* dst = reinterpret_cast<uint32_t*>(packed + row * nbytes + g * 4 * BITS);
@@ -272,8 +283,8 @@ quantize_meta_kernel(QuantParams p) {
     const int64_t r = i / p.ngroups;
     const int64_t g = i - r * p.ngroups;
     const GroupStats s = group_stats(p, row_offset(p, r), g);
-    p.scale[i] = pk_f2h(s.scale);
-    p.mins[i] = pk_f2h(s.mn);
+    p.scale[meta_index(p, r, g)] = pk_f2h(s.scale);
+    p.mins[meta_index(p, r, g)] = pk_f2h(s.mn);
   }
 }
 
@@ -382,15 +393,21 @@ extern "C" int pk_unpack_low_bits(const uint8_t* packed, int64_t rows, int64_t p
 extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_t* shape,
                                 const int64_t* strides, int axis, int bits, int group_size,
                                 uint8_t* out_packed, uint16_t* out_scale, uint16_t* out_mins,
-                                void* stream) {
+                                int meta_layout, void* stream) {
   pk::clear_error();
   if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
   if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16 && dtype != PK_DTYPE_F32)
     return pk::fail("x must be float16, bfloat16 or float32");
   if (ndim < 1 || ndim > kMaxDims) return pk::fail("x must have 1..8 dims");
   if (axis < 0 || axis >= ndim) return pk::fail("axis out of range");
+  if (meta_layout != PK_META_CHANNEL_MAJOR && meta_layout != PK_META_GROUP_MAJOR)
+    return pk::fail("meta_layout must be PK_META_CHANNEL_MAJOR or PK_META_GROUP_MAJOR");
+  if (meta_layout == PK_META_GROUP_MAJOR && (ndim < 2 || axis != ndim - 2))
+    return pk::fail("group-major scale/mins need axis == ndim - 2");
   QuantParams p{};
   p.x = x;
+  p.meta_gm = meta_layout == PK_META_GROUP_MAJOR;
+  p.meta_d = ndim >= 2 ? shape[ndim - 1] : 1;
   p.dtype = dtype;
   p.len = shape[axis];
   p.ax_stride = strides[axis];
@@ -434,7 +451,7 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
   }
   const bool fast = dtype == PK_DTYPE_F16 && contiguous && group_size == 32 && p.len % 32 == 0 &&
                     reinterpret_cast<uintptr_t>(x) % 16 == 0;
-  if (fast && axis == ndim - 1) {
+  if (fast && axis == ndim - 1 && !p.meta_gm) {
     const int64_t groups = p.rows * p.ngroups;
 #define PK_INNER(B) hipLaunchKernelGGL(quantize_inner32_kernel<B>, dim3(grid_for(groups)), dim3(kThreads), \
                                        0, s, static_cast<const uint16_t*>(x), p.rows, p.len, p.ngroups, \
@@ -449,7 +466,7 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
     const int64_t threads = outer * p.ngroups * (D / 2);
 #define PK_OUTER(B) hipLaunchKernelGGL(quantize_outer32_kernel<B>, dim3(grid_for(threads)), dim3(kThreads), \
                                        0, s, static_cast<const uint16_t*>(x), outer, p.len, D, p.ngroups, \
-                                       p.nbytes, out_packed, out_scale, out_mins)
+                                       p.nbytes, out_packed, out_scale, out_mins, p.meta_gm)
     if (bits == 2) PK_OUTER(2); else if (bits == 4) PK_OUTER(4); else PK_OUTER(8);
 #undef PK_OUTER
     return pk::check_launch("quantize_pack");

@@ -31,6 +31,14 @@ def _inner_contiguous(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+def _group_major(t: torch.Tensor) -> bool:
+    """``t`` [..., D, n_groups] is the transposed view of dense [..., n_groups, D] storage."""
+    if t.dim() < 2:
+        return False
+    d, g = t.shape[-2], t.shape[-1]
+    return d > 1 and t.stride(-2) == 1 and (g <= 1 or t.stride(-1) == d)
+
+
 def _bh_strides(t: torch.Tensor, batched: bool) -> Tuple[int, int]:
     """(batch stride, head stride) in elements of a [B, H, ...] or [H, ...] tensor."""
     if batched:
@@ -77,16 +85,24 @@ def packed_segment(key, value, *, batched: bool, splits: int = 0, split_len: int
         raise ValueError("packed K/V segment is empty")
     dev = _lib.require_device(key.packed, key.scale, key.mins, value.packed, value.scale,
                               value.mins)
-    kp, ks, km = (_inner_contiguous(t) for t in (key.packed, key.scale, key.mins))
+    kp = _inner_contiguous(key.packed)
+    if kind == _lib.PK_SEG_KIVI and _group_major(key.scale) and _group_major(key.mins) \
+            and key.scale.stride() == key.mins.stride():
+        ks, km, meta_layout = key.scale, key.mins, _lib.PK_META_GROUP_MAJOR
+    else:
+        ks, km = (_inner_contiguous(t) for t in (key.scale, key.mins))
+        meta_layout = _lib.PK_META_CHANNEL_MAJOR
     vp, vs, vm = (_inner_contiguous(t) for t in (value.packed, value.scale, value.mins))
     if ks.stride() != km.stride() or vs.stride() != vm.stride():
         ks, km, vs, vm = ks.contiguous(), km.contiguous(), vs.contiguous(), vm.contiguous()
+        meta_layout = _lib.PK_META_CHANNEL_MAJOR
     d = _lib.PkSegment()
     d.kind = kind
     d.length = s_len
     d.k_bits, d.v_bits = key.bits, value.bits
     d.k_group, d.v_group = key.group_size, value.group_size
     d.splits, d.split_len = int(splits), int(split_len)
+    d.k_meta_layout, d.reserved = meta_layout, 0
     d.seq_lens = 0 if seq_lens is None else seq_lens.data_ptr()
     d.k_data, d.k_scale, d.k_mins = kp.data_ptr(), ks.data_ptr(), km.data_ptr()
     d.v_data, d.v_scale, d.v_mins = vp.data_ptr(), vs.data_ptr(), vm.data_ptr()
