@@ -73,14 +73,15 @@ int pk_unpack_low_bits(const uint8_t* packed, int64_t rows, int64_t packed_len, 
  * resolved by the caller to gs = min(group_size, len) (or len).  Outputs are
  * contiguous in the moved layout: out_packed [rows, ceil(len/vpb)],
  * out_scale/out_mins fp16 [rows, ceil(len/gs)], rows = prod(shape) / len in
- * the original order of the remaining dims (meta_layout PK_META_CHANNEL_MAJOR),
- * or, for axis == ndim - 2 only, that array's last two dims transposed
- * (PK_META_GROUP_MAJOR: [rows / D, ceil(len/gs), D], D = shape[ndim - 1]).
- * Bit-exact with the reference. */
+ * the original order of the remaining dims.  For axis == ndim - 2 only, the
+ * layout flags PK_LAYOUT_META_TRANSPOSED / PK_LAYOUT_CODES_TRANSPOSED store
+ * scale / mins resp. the codes with those arrays' last two dims transposed
+ * ([rows / D, ceil(len/gs), D] and [rows / D, ceil(len/vpb), D], D =
+ * shape[ndim - 1]).  Bit-exact with the reference. */
 int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_t* shape,
                      const int64_t* strides, int axis, int bits, int group_size,
                      uint8_t* out_packed, uint16_t* out_scale, uint16_t* out_mins,
-                     int meta_layout, void* stream);
+                     int layout, void* stream);
 
 /* unpack_dequantize (packing.py:158-175): inverse of pk_quantize_pack.  Writes
  * fp16 out contiguous in the ORIGINAL layout orig_shape (ndim <= 8), with
@@ -95,13 +96,20 @@ int pk_unpack_dequantize(const uint8_t* packed, const uint16_t* scale, const uin
  * dims of packed / meta buffers are contiguous.  For PK_SEG_FP16 the K/V data
  * pointers are fp16 and k_meta / v_meta strides are unused; tok_stride is the
  * element stride between tokens (hd is contiguous). */
-/* Storage of a KIVI K segment's scale / min (logical shape [..., head_dim, groups]):
- * channel major is the reference's contiguous layout; group major stores the
- * transpose, [..., groups, head_dim] contiguous, so that the scales of a few
- * consecutive groups of every channel are one contiguous run.  pk_quantize_pack
- * writes either; the decode kernels read either. */
+/* Storage of a KIVI K segment (packed along tokens; logical shapes codes
+ * [..., head_dim, bytes] and scale / min [..., head_dim, groups]).  Channel major
+ * is the reference's contiguous layout.  The transposed storage keeps every
+ * channel of one token byte (codes) or one group (scale / min) together,
+ * [..., bytes, head_dim] and [..., groups, head_dim] contiguous, so that a few
+ * consecutive tokens of all channels are one contiguous run.  pk_quantize_pack
+ * writes either (for the second-to-last axis); the decode kernels read either. */
 #define PK_META_CHANNEL_MAJOR 0
 #define PK_META_GROUP_MAJOR 1
+#define PK_CODES_CHANNEL_MAJOR 0
+#define PK_CODES_TOKEN_MAJOR 1
+/* pk_quantize_pack layout flags */
+#define PK_LAYOUT_META_TRANSPOSED 1
+#define PK_LAYOUT_CODES_TRANSPOSED 2
 
 typedef struct pk_segment {
   int32_t kind;            /* PK_SEG_* */
@@ -113,7 +121,7 @@ typedef struct pk_segment {
                               split_len tokens are launched (trailing ones may be empty, like
                               attention_triton.py:227-240); 0 = split_len = ceil(len / splits) */
   int32_t k_meta_layout;   /* KIVI K scale/min storage: PK_META_CHANNEL_MAJOR or PK_META_GROUP_MAJOR */
-  int32_t reserved;        /* 0 */
+  int32_t k_data_layout;   /* KIVI K code storage: PK_CODES_CHANNEL_MAJOR or PK_CODES_TOKEN_MAJOR */
   const int32_t* seq_lens; /* device [batch] valid tokens per row, or NULL (= length) */
   const void* k_data; const uint16_t* k_scale; const uint16_t* k_mins;
   const void* v_data; const uint16_t* v_scale; const uint16_t* v_mins;

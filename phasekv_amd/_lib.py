@@ -31,6 +31,10 @@ PK_FLAG_GENERIC_KERNEL = 1
 
 PK_META_CHANNEL_MAJOR = 0
 PK_META_GROUP_MAJOR = 1
+PK_CODES_CHANNEL_MAJOR = 0
+PK_CODES_TOKEN_MAJOR = 1
+PK_LAYOUT_META_TRANSPOSED = 1
+PK_LAYOUT_CODES_TRANSPOSED = 2
 
 _c_i32 = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -43,7 +47,7 @@ class PkSegment(ctypes.Structure):
     _fields_ = [
         ("kind", _c_i32), ("length", _c_i32), ("k_bits", _c_i32), ("v_bits", _c_i32),
         ("k_group", _c_i32), ("v_group", _c_i32), ("splits", _c_i32), ("split_len", _c_i32),
-        ("k_meta_layout", _c_i32), ("reserved", _c_i32),
+        ("k_meta_layout", _c_i32), ("k_data_layout", _c_i32),
         ("seq_lens", _c_vp),
         ("k_data", _c_vp), ("k_scale", _c_vp), ("k_mins", _c_vp),
         ("v_data", _c_vp), ("v_scale", _c_vp), ("v_mins", _c_vp),

@@ -45,6 +45,7 @@ struct SegDev {
   int gbegin;         // index of its first chunk among all chunks of a (batch, kv head)
   int lbegin;         // index of its first chunk within this launch (blockIdx.x)
   int kmeta_gm;       // KIVI K scale/min stored group major ([groups][hd] per batch row, kv head)
+  int kdata_tm;       // KIVI K codes stored token-byte major ([bytes][hd] per batch row, kv head)
   int hd_meta;        // head_dim (the group-major row length)
   const int32_t* seq_lens;
   const uint8_t* kd; const uint16_t* ks; const uint16_t* km;

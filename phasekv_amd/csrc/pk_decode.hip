@@ -33,7 +33,8 @@ __device__ __forceinline__ float kivi_k_elem(const SegDev& s, int64_t kd_off, in
   const int vpb = 8 / s.kbits;
   const int64_t row_bytes = (s.length + vpb - 1) / vpb;
   const int64_t row_groups = (s.length + s.kgs - 1) / s.kgs;
-  const uint32_t byte = s.kd[kd_off + d * row_bytes + tok / vpb];
+  const uint32_t byte = s.kd[kd_off + (s.kdata_tm ? (int64_t)(tok / vpb) * s.hd_meta + d
+                                                 : d * row_bytes + tok / vpb)];
   const uint32_t code = (byte >> ((tok % vpb) * s.kbits)) & ((1u << s.kbits) - 1u);
   const int64_t g = s.kmeta_gm ? (int64_t)(tok / s.kgs) * s.hd_meta + d : d * row_groups + tok / s.kgs;
   return static_cast<float>(code) * pk_h2f(s.ks[km_off + g]) + pk_h2f(s.km[km_off + g]);
@@ -321,6 +322,9 @@ static int validate_problem(const pk_decode_problem* p) {
     if (s.k_meta_layout != PK_META_CHANNEL_MAJOR &&
         (s.k_meta_layout != PK_META_GROUP_MAJOR || s.kind != PK_SEG_KIVI))
       return fail("k_meta_layout must be channel major, or group major for a KIVI segment");
+    if (s.k_data_layout != PK_CODES_CHANNEL_MAJOR &&
+        (s.k_data_layout != PK_CODES_TOKEN_MAJOR || s.kind != PK_SEG_KIVI))
+      return fail("k_data_layout must be channel major, or token major for a KIVI segment");
     if (s.v_group > hd) return fail("V group size exceeds head_dim");
     if (s.kind == PK_SEG_TOKEN && s.k_group > hd) return fail("K group size exceeds head_dim");
   }
@@ -362,6 +366,10 @@ static bool mfma_eligible(const pk_decode_problem* p) {
       continue;
     }
     if (s.kind != PK_SEG_KIVI) return false;
+    // token-major K codes are read in 16-byte pieces of HD-byte rows
+    if (s.k_data_layout == PK_CODES_TOKEN_MAJOR &&
+        (!aligned(s.k_data, 16) || s.k_data_bstride % 16 || s.k_data_hstride % 16))
+      return false;
     // K groups of 32 tokens, or one group for a segment of at most 32 tokens
     if (!(s.k_group == 32 || (s.length <= 32 && s.k_group >= s.length)) || s.v_group != 32)
       return false;
@@ -465,6 +473,7 @@ static void fill_segment(SegDev& d, const pk_segment& s) {
   d.vm_bs = s.v_meta_bstride; d.vm_hs = s.v_meta_hstride;
   d.tok_stride = s.tok_stride;
   d.kmeta_gm = s.kind == PK_SEG_KIVI && s.k_meta_layout == PK_META_GROUP_MAJOR;
+  d.kdata_tm = s.kind == PK_SEG_KIVI && s.k_data_layout == PK_CODES_TOKEN_MAJOR;
 }
 
 static size_t generic_lds_bytes(const Plan& pl, int hd) {

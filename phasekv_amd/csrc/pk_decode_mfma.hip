@@ -154,7 +154,9 @@ __device__ __forceinline__ float lazy_rescale(WaveAcc<HD>& acc, float mt) {
 // The store to LDS transposes what the matrix operands need transposed:
 //   Kw  uint32 [4 KB][HD + 16/KB]  word w of every channel's K codes; the row
 //                                  padding puts the KB pieces a wave stores
-//                                  at once in distinct banks
+//                                  at once in distinct banks (channel-major codes)
+//   Kt  bytes [16 KB][HD + 16]     token-major codes as stored: byte row j holds
+//                                  the j-th code byte of every channel
 //   Ks, Km  fp16 [4][HD]           K scale / min of the stage's groups
 //   V   VB = 8: [128][HD*VB/8] the stage's V rows as stored.  VB = 2, 4: per
 //       group [word w][byte b][token pair tp] uint32 = (byte b of word w of
@@ -170,7 +172,10 @@ constexpr int kStage = 128;
 template <int HD, int KB, int VB>
 struct StageLayout {
   static constexpr int kw_row = HD + 16 / KB;             // words per Kw row
-  static constexpr int kw_bytes = 4 * KB * kw_row * 4;
+  // token-major codes: 16 KB byte rows of HD channels, rows padded to 16-byte multiples
+  static constexpr int kt_pitch = HD + 16;
+  static constexpr int kt_bytes = 16 * KB * kt_pitch;
+  static constexpr int kw_bytes = (4 * KB * kw_row * 4 > kt_bytes) ? 4 * KB * kw_row * 4 : kt_bytes;
   static constexpr int off_ks = kw_bytes;
   static constexpr int off_km = off_ks + 4 * HD * 2;
   static constexpr int off_vw = off_km + 4 * HD * 2;
@@ -242,6 +247,8 @@ struct KivLoad {
   bool kmeta4;         // channel major: the 4 group scales of a stage are one aligned 8-byte load
   bool kmeta_gm;       // group major: a stage's scales are [4][HD] contiguous (8-byte loads)
   bool gm_elems;       // group major but not 8-byte aligned: per-element loads
+  bool kdata_tm;       // token-major K codes: a stage is 16 KB rows of HD bytes, contiguous
+  int64_t k_rows;      // token-major: code byte rows of the segment
 };
 
 // K scale/min of a stage: in lane order.  Channel major: lane (tensor, channel)
@@ -286,6 +293,16 @@ __device__ __forceinline__ void load_stage(StageRegs<HD, KB, VB>& r, const SegDe
   using L = StageLayout<HD, KB, VB>;
   const int64_t byte0 = (int64_t)ts * KB / 8;
   const uint8_t* krows = s.kd + o.kd;
+  if (kl.kdata_tm) {
+    // the stage's byte rows are contiguous; pieces past the last row repeat it
+    const int64_t last = (kl.k_rows - byte0) * (HD / 16) - 1;
+#pragma unroll
+    for (int i = 0; i < R::NK; ++i) {
+      const int q = tid + kThreads * i;
+      if (R::KP % kThreads == 0 || q < R::KP)
+        r.k[i] = *reinterpret_cast<const u4_t*>(krows + byte0 * HD + min((int64_t)q, last) * 16);
+    }
+  } else
 #pragma unroll
   for (int i = 0; i < R::NK; ++i) {
     const int q = tid + kThreads * i;
@@ -336,8 +353,9 @@ __device__ __forceinline__ void load_stage(StageRegs<HD, KB, VB>& r, const SegDe
 template <int HD, int KB, int VB>
 struct FastOffsets {
   uint32_t krow[StageRegs<HD, KB, VB>::NK];   // channel row start of each K piece
-  uint32_t mrow;                             // K metadata: lane offset (elements)
-  uint32_t mstep;                            // K metadata: elements per group (1 or HD)
+  uint32_t mrow;                             // K metadata: channel-major lane offset (elements)
+  uint32_t mgrp;                             // K metadata, group major: the lane's group in the stage
+  uint32_t mcol;                             // K metadata, group major: the lane's first channel
 };
 
 // Stage loads for segments whose K rows are 16-byte aligned and hold a
@@ -355,17 +373,25 @@ __device__ __forceinline__ void load_stage_fast(StageRegs<HD, KB, VB>& r, const 
   const uint32_t byte0 = (uint32_t)ts * KB / 8;
   const uint32_t kmax = (uint32_t)kl.row_bytes - 16;
   const uint8_t* krows = s.kd + o.kd;
+  // token-major: the stage's rows are contiguous from byte0 * HD, the last piece
+  // repeated past the segment's last row; channel-major: one row span per channel
+  const uint32_t tlast = (uint32_t)((kl.k_rows - byte0) * (HD / 16)) - 1;
 #pragma unroll
   for (int i = 0; i < R::NK; ++i) {
+    const uint32_t q = (uint32_t)((tid + kThreads * i) & (R::KP - 1));
     const uint32_t kj = 16u * ((tid + kThreads * i) % KB);   // piece within the row span
-    r.k[i] = *reinterpret_cast<const u4_t*>(krows + fo.krow[i] + min(byte0 + kj, kmax));
+    const uint32_t off = kl.kdata_tm ? byte0 * HD + 16u * min(q, tlast)
+                                     : fo.krow[i] + min(byte0 + kj, kmax);
+    r.k[i] = *reinterpret_cast<const u4_t*>(krows + off);
   }
   {
-    // both layouts are one aligned 8-byte load per lane; fo.mrow / fo.mstep
-    // hold the layout's lane offset and per-group step
+    // both layouts are one aligned 8-byte load per lane; group major clamps the
+    // lane's group to the segment's last one
     const int q = tid & (2 * HD - 1);
     const uint16_t* m = pick(q < HD, s.ks, s.km) + o.km;
-    r.km = *reinterpret_cast<const u2_t*>(m + fo.mrow + (ts / 32) * fo.mstep);
+    const uint32_t g = min((uint32_t)(ts / 32) + fo.mgrp, (uint32_t)kl.row_groups - 1u);
+    const uint32_t off = kl.kmeta_gm ? g * HD + fo.mcol : fo.mrow + (uint32_t)(ts / 32);
+    r.km = *reinterpret_cast<const u2_t*>(m + off);
   }
   if constexpr (R::spread) {
     load_vslices<HD, KB, VB>(r, s.vd + o.vd, ts, t_last, tid);
@@ -387,11 +413,19 @@ __device__ __forceinline__ void load_stage_fast(StageRegs<HD, KB, VB>& r, const 
 }
 
 template <int HD, int KB, int VB>
-__device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, bool kmeta_gm, int tid,
-                                            char* st) {
+__device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, bool kmeta_gm,
+                                            bool kdata_tm, int tid, char* st) {
   using L = StageLayout<HD, KB, VB>;
   using R = StageRegs<HD, KB, VB>;
   uint32_t* kw = reinterpret_cast<uint32_t*>(st);
+  if (kdata_tm) {
+#pragma unroll
+    for (int i = 0; i < R::NK; ++i) {
+      const int q = tid + kThreads * i;
+      if (R::KP % kThreads == 0 || q < R::KP)
+        *reinterpret_cast<u4_t*>(st + (q / (HD / 16)) * L::kt_pitch + (q % (HD / 16)) * 16) = r.k[i];
+    }
+  } else
 #pragma unroll
   for (int i = 0; i < R::NK; ++i) {
     const int q = tid + kThreads * i;
@@ -480,10 +514,12 @@ __device__ __forceinline__ int pv_slot(int h, int e) {
 // one staged 32-token KIVI group
 // ---------------------------------------------------------------------------
 template <int HD, int KB, int VB, bool FULL>
-__device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, const u4_t (&qb)[HD / 32],
-                           WaveAcc<HD>& acc, float sl2, int lane) {
+__device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, bool ktm,
+                                           const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc, float sl2,
+                                           int lane) {
   using L = StageLayout<HD, KB, VB>;
   const char* kwg = st + grp * KB * L::kw_row * 4;        // the group's Kw rows
+  const char* ktg = st + grp * 4 * KB * L::kt_pitch;      // the group's Kt byte rows
   const char* ksg = st + L::off_ks + grp * HD * 2;
   const char* kmg = st + L::off_km + grp * HD * 2;
   const char* vsg = st + L::off_vs + grp * kTile * 2;     // channel group stride kStage
@@ -508,7 +544,46 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
   const float bias = db[0] * sl2;
   // ---- S^T = codes_K * q' for instances h = 0, 1 (16 tokens each) ----
   f4_t d[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  if constexpr (KB == 8) {
+  if (ktm) {
+    // token-major codes: one 8-byte read gives this lane's 8 channels of a code
+    // byte row; byte pairs (2m, 2m + 1) go to the two fp16 halves of operand m
+    uint32_t mask[2];
+    if (KB == 2) {
+      mask[0] = 0x00030003u << (2 * (r & 1));
+      mask[1] = 0x00030003u << (2 * (2 + (r & 1)));
+    } else {
+      mask[0] = 0x000F000Fu;
+      mask[1] = 0x00F000F0u;
+    }
+    const uint32_t sel0 = 0u | (0x0cu << 8) | (1u << 16) | (0x0cu << 24);
+    const uint32_t sel1 = 2u | (0x0cu << 8) | (3u << 16) | (0x0cu << 24);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // code byte row of token qk_token(h, r): r / 2 (2-bit), r (4-bit), 16 h + r (8-bit)
+        if (KB != 8 && h == 1) break;
+        const int row = (KB == 2) ? (r >> 1) : (KB == 4) ? r : 16 * h + r;
+        const u2_t x = lds_u2(ktg + row * L::kt_pitch + 32 * s + 8 * g4);
+        uint32_t u[4];
+        u[0] = perm(x[0], x[0], sel0);
+        u[1] = perm(x[0], x[0], sel1);
+        u[2] = perm(x[1], x[1], sel0);
+        u[3] = perm(x[1], x[1], sel1);
+        if constexpr (KB == 8) {
+          d[h] = mfma(u4_t{u[0], u[1], u[2], u[3]}, qp[s], d[h]);
+        } else {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            u4_t a;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) a[m] = u[m] & mask[hh];
+            d[hh] = mfma(a, qp[s], d[hh]);
+          }
+        }
+      }
+    }
+  } else if constexpr (KB == 8) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
@@ -734,14 +809,14 @@ __device__ __forceinline__ void fp16_group(const uint16_t* kbase, const uint16_t
 // one 32-token group of stage i (wave w computes group w of each stage)
 template <int HD, int KB, int VB>
 __device__ __forceinline__ void stage_group(const char* st, int i, int t_first, int t_stride,
-                                            int t_end, int wave, int lane,
+                                            int t_end, bool ktm, int wave, int lane,
                                             const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
                                             float sl2) {
   const int t0 = t_first + i * t_stride + kTile * wave;
   if (t0 < t_end) {
     const int nvalid = min(kTile, t_end - t0);
-    if (nvalid == kTile) kivi_group<HD, KB, VB, true>(nvalid, st, wave, qb, acc, sl2, lane);
-    else kivi_group<HD, KB, VB, false>(nvalid, st, wave, qb, acc, sl2, lane);
+    if (nvalid == kTile) kivi_group<HD, KB, VB, true>(nvalid, st, wave, ktm, qb, acc, sl2, lane);
+    else kivi_group<HD, KB, VB, false>(nvalid, st, wave, ktm, qb, acc, sl2, lane);
   }
 }
 
@@ -768,13 +843,11 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
       const int q = (tid + kThreads * i) & (R::KP - 1);
       fo.krow[i] = (uint32_t)((q / KB) * kl.row_bytes);
     }
-    if (kl.kmeta_gm) {
+    {
       const int q = tid & (HD - 1);
-      fo.mrow = (uint32_t)((q / (HD / 4)) * HD + 4 * (q & (HD / 4 - 1)));
-      fo.mstep = HD;
-    } else {
-      fo.mrow = (uint32_t)((tid & (HD - 1)) * kl.row_groups);
-      fo.mstep = 1;
+      fo.mgrp = (uint32_t)(q / (HD / 4));
+      fo.mcol = (uint32_t)(4 * (q & (HD / 4 - 1)));
+      fo.mrow = (uint32_t)(q * kl.row_groups);
     }
   }
   auto load = [&](R& r, int st) {
@@ -798,31 +871,31 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
     // stage 0 goes out alone: every workgroup starts at once, and its first
     // stage should not queue behind everybody's next ones
     load(ra, 0);
-    store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, buf0);
+    store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, buf0);
     if (nst > 1) load(rb, 1);
     if (nst > 2) load(ra, 2);
     __syncthreads();
     // steady state: stages i + 1 and i + 2 in flight, i + 3 and i + 4 loaded here
     for (; i + 4 < nst; i += 2) {
-      stage_group<HD, KB, VB>(buf0, i, t_first, t_stride, t_end, wave, lane, qb, acc, sl2);
-      store_stage<HD, KB, VB>(rb, kl.kmeta_gm, tid, buf1);
+      stage_group<HD, KB, VB>(buf0, i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb, acc, sl2);
+      store_stage<HD, KB, VB>(rb, kl.kmeta_gm, kl.kdata_tm, tid, buf1);
       load(rb, i + 3);
       __syncthreads();
-      stage_group<HD, KB, VB>(buf1, i + 1, t_first, t_stride, t_end, wave, lane, qb, acc, sl2);
-      store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, buf0);
+      stage_group<HD, KB, VB>(buf1, i + 1, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb, acc, sl2);
+      store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, buf0);
       load(ra, i + 4);
       __syncthreads();
     }
     // tail: at most four stages left, none loaded beyond nst
     for (; i < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, wave, lane, qb,
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb,
                               acc, sl2);
       if (i + 1 < nst) {
         if (i & 1) {
-          store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, buf0);
+          store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, buf0);
           if (i + 3 < nst) load(ra, i + 3);
         } else {
-          store_stage<HD, KB, VB>(rb, kl.kmeta_gm, tid, buf1);
+          store_stage<HD, KB, VB>(rb, kl.kmeta_gm, kl.kdata_tm, tid, buf1);
           if (i + 3 < nst) load(rb, i + 3);
         }
         __syncthreads();
@@ -830,21 +903,21 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
     }
   } else {
     load(ra, 0);
-    store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, buf0);
+    store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, buf0);
     if (nst > 1) load(ra, 1);
     __syncthreads();
     for (; i + 2 < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, wave, lane, qb,
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb,
                               acc, sl2);
-      store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, (i & 1) ? buf0 : buf1);
+      store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, (i & 1) ? buf0 : buf1);
       load(ra, i + 2);
       __syncthreads();
     }
     for (; i < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, wave, lane, qb,
+      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb,
                               acc, sl2);
       if (i + 1 < nst) {
-        store_stage<HD, KB, VB>(ra, kl.kmeta_gm, tid, (i & 1) ? buf0 : buf1);
+        store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, (i & 1) ? buf0 : buf1);
         __syncthreads();
       }
     }
@@ -861,9 +934,13 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
   KivLoad kl;
   kl.row_bytes = ((int64_t)s.length * KB + 7) / 8;
   kl.row_groups = (s.length + s.kgs - 1) / s.kgs;
+  kl.k_rows = kl.row_bytes;
   const int64_t byte_begin = (int64_t)t_first * KB / 8;
   const uintptr_t kaddr = reinterpret_cast<uintptr_t>(s.kd + o.kd);
-  if (kl.row_bytes % 16 == 0 && byte_begin % 16 == 0 && kaddr % 16 == 0) kl.kmode = 16;
+  // token-major rows are HD bytes (the host sends only 16-byte aligned ones here)
+  kl.kdata_tm = s.kdata_tm;
+  if (kl.kdata_tm) kl.kmode = 16;
+  else if (kl.row_bytes % 16 == 0 && byte_begin % 16 == 0 && kaddr % 16 == 0) kl.kmode = 16;
   else if (kl.row_bytes % 4 == 0 && byte_begin % 4 == 0 && kaddr % 4 == 0) kl.kmode = 4;
   else kl.kmode = 1;
   const bool meta8 = (reinterpret_cast<uintptr_t>(s.ks + o.km) % 8 == 0) &&
@@ -872,10 +949,7 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
   kl.gm_elems = s.kmeta_gm && !meta8;
   kl.kmeta4 = !s.kmeta_gm && (kl.row_groups % 4 == 0) && (t_first % kStage == 0) &&
               (t_stride % kStage == 0) && meta8;
-  // the fast loads take the stage's 4 groups unclamped: whole 4-group stages only
-  const bool gm_fast = kl.kmeta_gm && (kl.row_groups % 4 == 0) && (t_first % kStage == 0) &&
-                       (t_stride % kStage == 0);
-  if (kl.kmode == 16 && (kl.kmeta4 || gm_fast) && kl.row_bytes < ((int64_t)1 << 31) / HD)
+  if (kl.kmode == 16 && (kl.kmeta4 || kl.kmeta_gm) && kl.row_bytes < ((int64_t)1 << 31) / HD)
     kivi_stages<HD, KB, VB, true>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
                                   stage_bytes, qb, acc, sl2);
   else

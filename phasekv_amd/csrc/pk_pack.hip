@@ -74,6 +74,7 @@ struct QuantParams {
   int64_t rows;
   int rows_fastest;               // thread index -> (row fastest) or (group fastest)
   int meta_gm;                    // scale/mins group major over the last dim (axis == ndim - 2)
+  int codes_tm;                   // codes token-byte major over the last dim (axis == ndim - 2)
   int64_t meta_d;                 // that last dim
   uint8_t* packed;
   uint16_t* scale;
@@ -97,6 +98,13 @@ __device__ __forceinline__ int64_t meta_index(const QuantParams& p, int64_t r, i
   if (!p.meta_gm) return r * p.ngroups + g;
   const int64_t o = r / p.meta_d;
   return (o * p.ngroups + g) * p.meta_d + (r - o * p.meta_d);
+}
+
+// Byte b of row r of the codes: [rows][nbytes], or [rows / D][nbytes][D].
+__device__ __forceinline__ int64_t code_index(const QuantParams& p, int64_t r, int64_t b) {
+  if (!p.codes_tm) return r * p.nbytes + b;
+  const int64_t o = r / p.meta_d;
+  return (o * p.nbytes + b) * p.meta_d + (r - o * p.meta_d);
 }
 
 __device__ __forceinline__ float load_x(const QuantParams& p, int64_t off) {
@@ -156,14 +164,13 @@ quantize_groups_kernel(QuantParams p) {
     p.mins[meta_index(p, r, g)] = pk_f2h(s.mn);
     const int64_t begin = g * p.gs;
     const int64_t end = min(begin + p.gs, p.len);
-    uint8_t* dst = p.packed + r * p.nbytes;
     for (int64_t b0 = begin; b0 < end; b0 += vpb) {
       uint32_t byte = 0;
       for (int k = 0; k < vpb; ++k) {
         const int64_t pos = b0 + k;
         if (pos < end) byte |= quant_code(load_x(p, off + pos * p.ax_stride), s, p.bits) << (k * p.bits);
       }
-      dst[b0 / vpb] = static_cast<uint8_t>(byte);
+      p.packed[code_index(p, r, b0 / vpb)] = static_cast<uint8_t>(byte);
     }
   }
 }
@@ -241,7 +248,8 @@ template <int BITS>
 __global__ void __launch_bounds__(kThreads)
 quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t len, int64_t D,
                         int64_t ngroups, int64_t nbytes, uint8_t* __restrict__ packed,
-                        uint16_t* __restrict__ scale, uint16_t* __restrict__ mins, int meta_gm) {
+                        uint16_t* __restrict__ scale, uint16_t* __restrict__ mins, int meta_gm,
+                        int codes_tm) {
   const int64_t pairs = D / 2;
   const int64_t total = outer * ngroups * pairs;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -257,6 +265,7 @@ quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t l
       a[t] = pk_h2f((uint16_t)(q & 0xFFFFu));
       b[t] = pk_h2f((uint16_t)(q >> 16));
     }
+    uint32_t w2[2][BITS];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const float (&v)[32] = k ? b : a;
@@ -265,11 +274,22 @@ quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t l
       const int64_t mi = meta_gm ? (o * ngroups + g) * D + 2 * cp + k : row * ngroups + g;
       scale[mi] = pk_f2h(st.scale);
       mins[mi] = pk_f2h(st.mn);
-      uint32_t w[BITS];
-      pack32<BITS>(v, st, w);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(packed + row * nbytes + g * 4 * BITS);
+      pack32<BITS>(v, st, w2[k]);
+      if (!codes_tm) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(packed + row * nbytes + g * 4 * BITS);
 #pragma unroll
-      for (int j = 0; j < BITS; ++j) dst[j] = w[j];
+        for (int j = 0; j < BITS; ++j) dst[j] = w2[k][j];
+      }
+    }
+    if (codes_tm) {
+      // byte j of the group for both channels: one 2-byte store into [bytes][D]
+      uint8_t* base = packed + (o * nbytes + g * 4 * BITS) * D + 2 * cp;
+#pragma unroll
+      for (int j = 0; j < 4 * BITS; ++j) {
+        const uint32_t lo = (w2[0][j >> 2] >> (8 * (j & 3))) & 0xFFu;
+        const uint32_t hi = (w2[1][j >> 2] >> (8 * (j & 3))) & 0xFFu;
+        *reinterpret_cast<uint16_t*>(base + (int64_t)j * D) = (uint16_t)(lo | (hi << 8));
+      }
     }
   }
 }
@@ -308,7 +328,7 @@ quantize_bytes_kernel(QuantParams p) {
       if (g != cur_g) { s = group_stats(p, off, g); cur_g = g; }
       byte |= quant_code(load_x(p, off + pos * p.ax_stride), s, p.bits) << (k * p.bits);
     }
-    p.packed[i] = static_cast<uint8_t>(byte);
+    p.packed[code_index(p, r, j)] = static_cast<uint8_t>(byte);
   }
 }
 
@@ -393,20 +413,21 @@ extern "C" int pk_unpack_low_bits(const uint8_t* packed, int64_t rows, int64_t p
 extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_t* shape,
                                 const int64_t* strides, int axis, int bits, int group_size,
                                 uint8_t* out_packed, uint16_t* out_scale, uint16_t* out_mins,
-                                int meta_layout, void* stream) {
+                                int layout, void* stream) {
   pk::clear_error();
   if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
   if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16 && dtype != PK_DTYPE_F32)
     return pk::fail("x must be float16, bfloat16 or float32");
   if (ndim < 1 || ndim > kMaxDims) return pk::fail("x must have 1..8 dims");
   if (axis < 0 || axis >= ndim) return pk::fail("axis out of range");
-  if (meta_layout != PK_META_CHANNEL_MAJOR && meta_layout != PK_META_GROUP_MAJOR)
-    return pk::fail("meta_layout must be PK_META_CHANNEL_MAJOR or PK_META_GROUP_MAJOR");
-  if (meta_layout == PK_META_GROUP_MAJOR && (ndim < 2 || axis != ndim - 2))
-    return pk::fail("group-major scale/mins need axis == ndim - 2");
+  if (layout & ~(PK_LAYOUT_META_TRANSPOSED | PK_LAYOUT_CODES_TRANSPOSED))
+    return pk::fail("unknown layout flags");
+  if (layout && (ndim < 2 || axis != ndim - 2))
+    return pk::fail("transposed storage needs axis == ndim - 2");
   QuantParams p{};
   p.x = x;
-  p.meta_gm = meta_layout == PK_META_GROUP_MAJOR;
+  p.meta_gm = (layout & PK_LAYOUT_META_TRANSPOSED) != 0;
+  p.codes_tm = (layout & PK_LAYOUT_CODES_TRANSPOSED) != 0;
   p.meta_d = ndim >= 2 ? shape[ndim - 1] : 1;
   p.dtype = dtype;
   p.len = shape[axis];
@@ -451,7 +472,7 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
   }
   const bool fast = dtype == PK_DTYPE_F16 && contiguous && group_size == 32 && p.len % 32 == 0 &&
                     reinterpret_cast<uintptr_t>(x) % 16 == 0;
-  if (fast && axis == ndim - 1 && !p.meta_gm) {
+  if (fast && axis == ndim - 1 && !layout) {
     const int64_t groups = p.rows * p.ngroups;
 #define PK_INNER(B) hipLaunchKernelGGL(quantize_inner32_kernel<B>, dim3(grid_for(groups)), dim3(kThreads), \
                                        0, s, static_cast<const uint16_t*>(x), p.rows, p.len, p.ngroups, \
@@ -466,7 +487,7 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
     const int64_t threads = outer * p.ngroups * (D / 2);
 #define PK_OUTER(B) hipLaunchKernelGGL(quantize_outer32_kernel<B>, dim3(grid_for(threads)), dim3(kThreads), \
                                        0, s, static_cast<const uint16_t*>(x), outer, p.len, D, p.ngroups, \
-                                       p.nbytes, out_packed, out_scale, out_mins, p.meta_gm)
+                                       p.nbytes, out_packed, out_scale, out_mins, p.meta_gm, p.codes_tm)
     if (bits == 2) PK_OUTER(2); else if (bits == 4) PK_OUTER(4); else PK_OUTER(8);
 #undef PK_OUTER
     return pk::check_launch("quantize_pack");

@@ -32,7 +32,7 @@ def _inner_contiguous(t: torch.Tensor) -> torch.Tensor:
 
 
 def _group_major(t: torch.Tensor) -> bool:
-    """``t`` [..., D, n_groups] is the transposed view of dense [..., n_groups, D] storage."""
+    """``t`` [..., D, n] is the transposed view of dense [..., n, D] storage."""
     if t.dim() < 2:
         return False
     d, g = t.shape[-2], t.shape[-1]
@@ -85,7 +85,10 @@ def packed_segment(key, value, *, batched: bool, splits: int = 0, split_len: int
         raise ValueError("packed K/V segment is empty")
     dev = _lib.require_device(key.packed, key.scale, key.mins, value.packed, value.scale,
                               value.mins)
-    kp = _inner_contiguous(key.packed)
+    if kind == _lib.PK_SEG_KIVI and _group_major(key.packed):
+        kp, data_layout = key.packed, _lib.PK_CODES_TOKEN_MAJOR
+    else:
+        kp, data_layout = _inner_contiguous(key.packed), _lib.PK_CODES_CHANNEL_MAJOR
     if kind == _lib.PK_SEG_KIVI and _group_major(key.scale) and _group_major(key.mins) \
             and key.scale.stride() == key.mins.stride():
         ks, km, meta_layout = key.scale, key.mins, _lib.PK_META_GROUP_MAJOR
@@ -102,7 +105,7 @@ def packed_segment(key, value, *, batched: bool, splits: int = 0, split_len: int
     d.k_bits, d.v_bits = key.bits, value.bits
     d.k_group, d.v_group = key.group_size, value.group_size
     d.splits, d.split_len = int(splits), int(split_len)
-    d.k_meta_layout, d.reserved = meta_layout, 0
+    d.k_meta_layout, d.k_data_layout = meta_layout, data_layout
     d.seq_lens = 0 if seq_lens is None else seq_lens.data_ptr()
     d.k_data, d.k_scale, d.k_mins = kp.data_ptr(), ks.data_ptr(), km.data_ptr()
     d.v_data, d.v_scale, d.v_mins = vp.data_ptr(), vs.data_ptr(), vm.data_ptr()

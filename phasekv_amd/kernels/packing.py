@@ -117,12 +117,12 @@ def quantize_pack(x: torch.Tensor, bits: int, axis: int, group_size: int) -> Pac
     ``code = round_half_even((x - min) / scale)`` in IEEE float32, exactly as the
     reference.
 
-    For ``axis == -2`` (the cache's per-channel K layout) ``scale`` / ``mins`` keep
-    the reference's shape ``[..., D, n_groups]`` but are transposed views of
-    ``[..., n_groups, D]`` storage: the scales of consecutive groups of every
-    channel then sit together, which is how the decode kernels read them.
-    Values are identical; code that needs the reference's contiguous layout
-    calls ``.contiguous()``.
+    For ``axis == -2`` (the cache's per-channel K layout) ``packed``, ``scale`` and
+    ``mins`` keep the reference's shapes ``[..., D, n_bytes]`` / ``[..., D, n_groups]``
+    but are transposed views of ``[..., n_bytes, D]`` / ``[..., n_groups, D]``
+    storage: a few consecutive tokens of every channel then sit together, which
+    is how the decode kernels read them.  Values are identical; code that needs
+    the reference's contiguous layout calls ``.contiguous()``.
     """
     if bits not in _PACKABLE_BITS:
         raise ValueError(f"bits must be one of {_PACKABLE_BITS}, got {bits}")
@@ -141,14 +141,17 @@ def quantize_pack(x: torch.Tensor, bits: int, axis: int, group_size: int) -> Pac
     vpb = _BITS_PER_BYTE // bits
     n_bytes = -(-length // vpb)
     n_groups = -(-length // gs)
-    packed = torch.empty(*moved_prefix, n_bytes, dtype=torch.uint8, device=dev)
     group_major = x.dim() >= 2 and axis == x.dim() - 2
     if group_major:
-        # [..., n_groups, D] storage seen as [..., D, n_groups]
-        meta_shape = (*moved_prefix[:-1], n_groups, moved_prefix[-1])
+        # [..., n_bytes, D] / [..., n_groups, D] storage seen as [..., D, n_bytes] / [..., D, n_groups]
+        d_last = moved_prefix[-1]
+        packed = torch.empty(*moved_prefix[:-1], n_bytes, d_last, dtype=torch.uint8,
+                             device=dev).transpose(-1, -2)
+        meta_shape = (*moved_prefix[:-1], n_groups, d_last)
         scale = torch.empty(*meta_shape, dtype=torch.float16, device=dev).transpose(-1, -2)
         mins = torch.empty(*meta_shape, dtype=torch.float16, device=dev).transpose(-1, -2)
     else:
+        packed = torch.empty(*moved_prefix, n_bytes, dtype=torch.uint8, device=dev)
         scale = torch.empty(*moved_prefix, n_groups, dtype=torch.float16, device=dev)
         mins = torch.empty(*moved_prefix, n_groups, dtype=torch.float16, device=dev)
     if packed.numel():
@@ -158,8 +161,8 @@ def quantize_pack(x: torch.Tensor, bits: int, axis: int, group_size: int) -> Pac
         _lib.check(lib.pk_quantize_pack(x.data_ptr(), _DTYPE_CODES[x.dtype], x.dim(), shape,
                                         strides, axis, bits, gs, packed.data_ptr(),
                                         scale.data_ptr(), mins.data_ptr(),
-                                        _lib.PK_META_GROUP_MAJOR if group_major
-                                        else _lib.PK_META_CHANNEL_MAJOR,
+                                        (_lib.PK_LAYOUT_META_TRANSPOSED
+                                         | _lib.PK_LAYOUT_CODES_TRANSPOSED) if group_major else 0,
                                         _lib.stream_ptr(dev)), "quantize_pack")
     return PackedTensor(packed=packed, scale=scale, mins=mins, bits=bits, axis=axis,
                         group_size=gs, orig_shape=orig_shape, axis_len=length)

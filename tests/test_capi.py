@@ -80,13 +80,13 @@ def test_python_side_rejects_bad_arguments_before_any_launch():
         packing.quantize_pack(x, 2, -1, 4)
 
 
-def test_group_major_metadata_only_for_the_second_innermost_axis():
-    """The ABI refuses group-major scale/min storage for any other axis, before any launch."""
+def test_transposed_storage_only_for_the_second_innermost_axis():
+    """The ABI refuses transposed code / scale storage for any other axis, before any launch."""
     lib = _lib.load()
     shape = _lib.i64_array((2, 64, 32))
     strides = _lib.i64_array((64 * 32, 32, 1))
     rc = lib.pk_quantize_pack(None, _lib.PK_DTYPE_F16, 3, shape, strides, 2, 2, 32, None, None,
-                              None, _lib.PK_META_GROUP_MAJOR, None)
+                              None, _lib.PK_LAYOUT_META_TRANSPOSED, None)
     assert rc == _lib.PK_ERR_INVALID
     assert b"axis == ndim - 2" in lib.pk_last_error()
     rc = lib.pk_quantize_pack(None, _lib.PK_DTYPE_F16, 3, shape, strides, 1, 2, 32, None, None,

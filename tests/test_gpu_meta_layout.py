@@ -1,6 +1,7 @@
-"""K scale/min storage: quantize_pack keeps the reference's shape and values for the
-per-channel K layout (axis -2) but stores the transpose; the decode kernels must give
-bit-identical results for that storage and for the reference's contiguous layout."""
+"""K code and scale/min storage: quantize_pack keeps the reference's shapes and values
+for the per-channel K layout (axis -2) but stores the transposes; the decode kernels must
+give bit-identical results for every mix of that storage and the reference's contiguous
+layout."""
 import dataclasses
 
 import numpy as np
@@ -16,6 +17,16 @@ def _contiguous_meta(pt):
     return dataclasses.replace(pt, scale=pt.scale.contiguous(), mins=pt.mins.contiguous())
 
 
+def _contiguous_codes(pt):
+    return dataclasses.replace(pt, packed=pt.packed.contiguous())
+
+
+def _layout_variants(pt):
+    """(codes token major, meta group major) x both: the four storages of one K segment."""
+    return {(1, 1): pt, (0, 1): _contiguous_codes(pt), (1, 0): _contiguous_meta(pt),
+            (0, 0): _contiguous_codes(_contiguous_meta(pt))}
+
+
 def test_quantize_pack_k_metadata_is_group_major_view_with_reference_values(gpu):
     from phasekv_amd.kernels.packing import quantize_pack
     g = torch.Generator().manual_seed(7)
@@ -24,6 +35,8 @@ def test_quantize_pack_k_metadata_is_group_major_view_with_reference_values(gpu)
     want = po.quantize_pack(x.numpy(), 2, -2, 32)
     assert tuple(pt.scale.shape) == want.scale.shape == (2, 3, 64, 7)
     assert pt.scale.stride(-2) == 1 and pt.scale.stride(-1) == 64      # [.., groups, D] storage
+    assert tuple(pt.packed.shape) == want.packed.shape == (2, 3, 64, 50)
+    assert pt.packed.stride(-2) == 1 and pt.packed.stride(-1) == 64     # [.., bytes, D] storage
     np.testing.assert_array_equal(pt.scale.cpu().numpy(), want.scale)
     np.testing.assert_array_equal(pt.mins.cpu().numpy(), want.mins)
     np.testing.assert_array_equal(pt.packed.cpu().numpy(), want.packed)
@@ -33,7 +46,7 @@ def test_quantize_pack_k_metadata_is_group_major_view_with_reference_values(gpu)
 
 
 @pytest.mark.parametrize("generic", [False, True])
-@pytest.mark.parametrize("lengths", [(4096, 256), (1000, 37), (384, 128, 33)])
+@pytest.mark.parametrize("lengths", [(4096, 256), (1000, 37), (384, 128, 33), (4000, 200, 96)])
 def test_decode_identical_for_both_metadata_layouts(gpu, generic, lengths):
     from phasekv_amd import decode as dec
     from phasekv_amd.kernels.packing import quantize_pack
@@ -41,22 +54,23 @@ def test_decode_identical_for_both_metadata_layouts(gpu, generic, lengths):
     g = torch.Generator().manual_seed(sum(lengths))
     hq, hkv, hd = 28, 4, 128
     q = torch.randn(1, hq, hd, generator=g).to(torch.float16).to(gpu)
-    gm_segs, cm_segs = [], []
+    segs = {key: [] for key in ((1, 1), (0, 1), (1, 0), (0, 0))}
     for i, length in enumerate(lengths):
-        bits = 2 if i == 0 else 4
+        bits = (2, 4, 8)[i % 3]
         k = torch.randn(1, hkv, length, hd, generator=g).to(torch.float16).to(gpu)
         v = torch.randn(1, hkv, length, hd, generator=g).to(torch.float16).to(gpu)
         pk, pv = quantize_pack(k, bits, -2, 32), quantize_pack(v, bits, -1, 32)
-        assert pk.scale.stride(-2) == 1
-        gm_segs.append(dec.packed_segment(pk, pv, batched=True))
-        cm_segs.append(dec.packed_segment(_contiguous_meta(pk), pv, batched=True))
-    assert gm_segs[0].desc.k_meta_layout == 1 and cm_segs[0].desc.k_meta_layout == 0
-    out_gm = dec.fused_decode(dec.Problem(q, gm_segs, hq, generic_kernel=generic))
-    out_cm = dec.fused_decode(dec.Problem(q, cm_segs, hq, generic_kernel=generic))
-    assert torch.equal(out_gm, out_cm)
-    pm_gm, pl_gm, pa_gm = dec.decode_partials(dec.Problem(q, gm_segs, hq, generic_kernel=generic))
-    pm_cm, pl_cm, pa_cm = dec.decode_partials(dec.Problem(q, cm_segs, hq, generic_kernel=generic))
-    assert torch.equal(pm_gm, pm_cm) and torch.equal(pl_gm, pl_cm) and torch.equal(pa_gm, pa_cm)
+        for key, variant in _layout_variants(pk).items():
+            seg = dec.packed_segment(variant, pv, batched=True)
+            assert (seg.desc.k_data_layout, seg.desc.k_meta_layout) == key
+            segs[key].append(seg)
+    ref = dec.fused_decode(dec.Problem(q, segs[(0, 0)], hq, generic_kernel=generic))
+    pref = dec.decode_partials(dec.Problem(q, segs[(0, 0)], hq, generic_kernel=generic))
+    for key in ((1, 1), (0, 1), (1, 0)):
+        out = dec.fused_decode(dec.Problem(q, segs[key], hq, generic_kernel=generic))
+        assert torch.equal(out, ref), key
+        part = dec.decode_partials(dec.Problem(q, segs[key], hq, generic_kernel=generic))
+        assert all(torch.equal(a, b) for a, b in zip(part, pref)), key
 
 
 def test_ragged_batch_identical_for_both_metadata_layouts(gpu):
@@ -69,10 +83,10 @@ def test_ragged_batch_identical_for_both_metadata_layouts(gpu):
     v = torch.randn(b, hkv, length, hd, generator=g).to(torch.float16).to(gpu)
     lens = torch.tensor([1024, 700, 129], dtype=torch.int32, device=gpu)
     pk, pv = quantize_pack(k, 2, -2, 32), quantize_pack(v, 2, -1, 32)
-    gm = dec.packed_segment(pk, pv, batched=True, seq_lens=lens)
-    cm = dec.packed_segment(_contiguous_meta(pk), pv, batched=True, seq_lens=lens)
-    assert torch.equal(dec.fused_decode(dec.Problem(q, [gm], hq)),
-                       dec.fused_decode(dec.Problem(q, [cm], hq)))
+    outs = [dec.fused_decode(dec.Problem(q, [dec.packed_segment(variant, pv, batched=True,
+                                                                seq_lens=lens)], hq))
+            for variant in _layout_variants(pk).values()]
+    assert all(torch.equal(o, outs[0]) for o in outs[1:])
 
 
 def test_unpack_dequantize_reads_group_major_metadata(gpu):
