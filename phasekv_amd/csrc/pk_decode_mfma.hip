@@ -1049,8 +1049,11 @@ decode_mfma_kernel(const DecodeParams p) {
   }
   // ---- wave results -> LDS, merge the 4 waves ----
   __syncthreads();
-  float* mo = reinterpret_cast<float*>(lds);               // [4][16][HD]
-  float* mm = mo + kWaves * 16 * HD;                        // [4][16]
+  // rows padded by 16 bytes: the 16 rows of one 16-byte store start 4 banks apart
+  // (unpadded, every row of a store would hit the same 4 banks)
+  constexpr int MP = HD + 4;
+  float* mo = reinterpret_cast<float*>(lds);               // [4][16][MP]
+  float* mm = mo + kWaves * 16 * MP;                        // [4][16]
   float* ml = mm + kWaves * 16;                             // [4][16]
   float l_full;
   if (s.kind == PK_SEG_FP16) {
@@ -1060,7 +1063,7 @@ decode_mfma_kernel(const DecodeParams p) {
     for (int e = 0; e < 4; ++e)
 #pragma unroll
       for (int bb = 0; bb < NB; bb += 4)
-        *reinterpret_cast<f4_t*>(mo + (wave * 16 + n) * HD + NB * (4 * g4 + e) + bb) =
+        *reinterpret_cast<f4_t*>(mo + (wave * 16 + n) * MP + NB * (4 * g4 + e) + bb) =
             f4_t{acc.o[bb][e], acc.o[bb + 1][e], acc.o[bb + 2][e], acc.o[bb + 3][e]};
   } else {
     // rows c < HD/32 of the bias product sit in lane group 0, row HD/32 in lane
@@ -1078,7 +1081,7 @@ decode_mfma_kernel(const DecodeParams p) {
       f[e] = kTwo24 / ((vb_bits == 2) ? (float)(1 << (2 * e)) : (vb_bits == 4) ? ((e & 1) ? 16.f : 1.f) : 1.f);
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb)
-      *reinterpret_cast<f4_t*>(mo + (wave * 16 + n) * HD + 16 * bb + 4 * g4) =
+      *reinterpret_cast<f4_t*>(mo + (wave * 16 + n) * MP + 16 * bb + 4 * g4) =
           acc.o[bb] * f + vbf[bb >> 1];
   }
   if (g4 == 0) {
@@ -1104,7 +1107,7 @@ decode_mfma_kernel(const DecodeParams p) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         const float wt = __builtin_amdgcn_exp2f(mw[w] - M);
-        o += wt * *reinterpret_cast<const f4_t*>(mo + (w * 16 + hh) * HD + c);
+        o += wt * *reinterpret_cast<const f4_t*>(mo + (w * 16 + hh) * MP + c);
         L += wt * ml[w * 16 + hh];
       }
     }
@@ -1137,7 +1140,7 @@ int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, in
   const int hd = dp.hd;
   dp.stage_lds = (kivi_stage_bytes(hd, max_kbits, max_vbits) + 15) & ~15;
   const size_t staging = 2 * (size_t)dp.stage_lds;
-  const size_t merge = sizeof(float) * ((size_t)kWaves * 16 * hd + 2 * kWaves * 16);
+  const size_t merge = sizeof(float) * ((size_t)kWaves * 16 * (hd + 4) + 2 * kWaves * 16);
   const size_t lds = std::max(staging, merge);
   dim3 grid(lchunks, dp.Hkv * dp.nslab, dp.B);
   const int maxb = std::max(max_kbits, max_vbits);
