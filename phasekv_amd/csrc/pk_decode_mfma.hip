@@ -172,8 +172,9 @@ constexpr int kStage = 128;
 template <int HD, int KB, int VB>
 struct StageLayout {
   static constexpr int kw_row = HD + 16 / KB;             // words per Kw row
-  // token-major codes: 16 KB byte rows of HD channels, rows padded to 16-byte multiples
-  static constexpr int kt_pitch = HD + 16;
+  // token-major codes: 16 KB byte rows of HD channels; the 8-byte pad puts rows
+  // r and r + 8 of an operand read in different banks
+  static constexpr int kt_pitch = HD + 8;
   static constexpr int kt_bytes = 16 * KB * kt_pitch;
   static constexpr int kw_bytes = (4 * KB * kw_row * 4 > kt_bytes) ? 4 * KB * kw_row * 4 : kt_bytes;
   static constexpr int off_ks = kw_bytes;
@@ -182,11 +183,26 @@ struct StageLayout {
   static constexpr int vrow_words = HD * VB / 32;
   static constexpr int vrow_bytes = HD * VB / 8;
   static constexpr bool vspread = VB != 8;
-  static constexpr int vgrp_words = vrow_words * 64 + 16;   // spread group stride (words)
+  // spread V (per group of 16 token pairs): dword (word w, byte b, token pair tp)
+  // at 64 s + 16 b + (tp ^ vswz(s, b)), s = vslot(w).  A lane stores the PW words
+  // of one slice qw of a token pair (NQ slices per row), and words are
+  // interleaved by slice, s = (w % PW) NQ + w / PW, so s and qw have the same
+  // parity.  With the store order of the byte rows (one half of the slices
+  // stores them as 1 0 3 2) the 32 stores of a half wave hit 32 banks, and the
+  // swizzle (bit 3 of tp, which keeps runs of 4 token pairs contiguous) puts
+  // byte rows b and b + 2 of an operand read in different banks.
+  static constexpr int vpw = (vrow_words >= 16) ? 4 : 2;
+  static constexpr int vnq = vrow_words / vpw;
+  static constexpr int vgrp_words = vrow_words * 64;           // spread group stride (words)
   static constexpr int vw_bytes = vspread ? 4 * vgrp_words * 4 : kStage * vrow_bytes;
+  // V scale / min rows of kStage tokens, padded so the rows of the bias
+  // operand read start 4 banks apart
+  static constexpr int vms = kStage + 8;
   static constexpr int off_vs = off_vw + vw_bytes;
-  static constexpr int off_vm = off_vs + (HD / 32) * kStage * 2;
-  static constexpr int bytes = off_vm + (HD / 32 + 1) * kStage * 2;
+  static constexpr int off_vm = off_vs + (HD / 32) * vms * 2;
+  static constexpr int bytes = off_vm + (HD / 32 + 1) * vms * 2;
+  __device__ static constexpr int vslot(int w) { return (w % vpw) * vnq + w / vpw; }
+  __device__ static constexpr int vswz(int s, int b) { return 8 * ((s ^ (b >> 1)) & 1); }
 };
 
 // One lane's share of a stage's global loads (256 lanes).
@@ -422,8 +438,11 @@ __device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, bool
 #pragma unroll
     for (int i = 0; i < R::NK; ++i) {
       const int q = tid + kThreads * i;
-      if (R::KP % kThreads == 0 || q < R::KP)
-        *reinterpret_cast<u4_t*>(st + (q / (HD / 16)) * L::kt_pitch + (q % (HD / 16)) * 16) = r.k[i];
+      if (R::KP % kThreads == 0 || q < R::KP) {
+        u2_t* dst = reinterpret_cast<u2_t*>(st + (q / (HD / 16)) * L::kt_pitch + (q % (HD / 16)) * 16);
+        dst[0] = u2_t{r.k[i][0], r.k[i][1]};
+        dst[1] = u2_t{r.k[i][2], r.k[i][3]};
+      }
     }
   } else
 #pragma unroll
@@ -454,12 +473,18 @@ __device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, bool
       const int q = tid + kThreads * i;
       if (R::VI % kThreads == 0 || q < R::VI) {
         const int tp = q / R::NQ, qw = q - tp * R::NQ;
-        uint32_t* dst = vsp + (tp >> 4) * L::vgrp_words + (tp & 15);
+        // slices in the upper half of each 4 (NQ = 4) or 2 (NQ = 2) store byte rows 1 0 3 2
+        const int flip = ((R::NQ == 4) ? (qw >> 1) : qw) & 1;
+        uint32_t* dst = vsp + (tp >> 4) * L::vgrp_words + qw * 64;
 #pragma unroll
         for (int k = 0; k < R::PW; ++k)
 #pragma unroll
-          for (int b = 0; b < 4; ++b)
-            dst[((qw * R::PW + k) * 4 + b) * 16] = perm(r.vb[i][k], r.va[i][k], sel_bytes(b));
+          for (int j = 0; j < 4; ++j) {
+            const int b = j ^ flip;
+            // slot k NQ + qw has the parity of qw; b >> 1 == j >> 1
+            const int sw = 8 * ((qw ^ (j >> 1)) & 1);
+            dst[k * R::NQ * 64 + b * 16 + ((tp & 15) ^ sw)] = perm(r.vb[i][k], r.va[i][k], sel_bytes(b));
+          }
       }
     }
   } else {
@@ -475,7 +500,7 @@ __device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, bool
     const int t = tid & (kStage - 1);
 #pragma unroll
     for (int cg = 0; cg < HD / 32; ++cg)
-      m[cg * kStage + t] = (uint16_t)(r.vm[cg >> 1] >> (16 * (cg & 1)));
+      m[cg * L::vms + t] = (uint16_t)(r.vm[cg >> 1] >> (16 * (cg & 1)));
   }
 }
 
@@ -522,7 +547,7 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
   const char* ktg = st + grp * 4 * KB * L::kt_pitch;      // the group's Kt byte rows
   const char* ksg = st + L::off_ks + grp * HD * 2;
   const char* kmg = st + L::off_km + grp * HD * 2;
-  const char* vsg = st + L::off_vs + grp * kTile * 2;     // channel group stride kStage
+  const char* vsg = st + L::off_vs + grp * kTile * 2;     // channel group stride vms
   const char* vmg = st + L::off_vm + grp * kTile * 2;
   constexpr int KS = HD / 32;
   constexpr int NB = HD / 16;
@@ -660,11 +685,11 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
   // 8 fp16 of channel-group row c of Vs / Vm for this lane's PV tokens
   auto vmeta8 = [&](const char* base, int c) -> u4_t {
     if constexpr (KB == 8) {
-      const u2_t x0 = lds_u2(base + (c * kStage + 4 * g4) * 2);
-      const u2_t x1 = lds_u2(base + (c * kStage + 16 + 4 * g4) * 2);
+      const u2_t x0 = lds_u2(base + (c * L::vms + 4 * g4) * 2);
+      const u2_t x1 = lds_u2(base + (c * L::vms + 16 + 4 * g4) * 2);
       return u4_t{x0[0], x0[1], x1[0], x1[1]};
     } else {
-      return lds_u4(base + (c * kStage + 8 * g4) * 2);
+      return lds_u4(base + (c * L::vms + 8 * g4) * 2);
     }
   };
   // ---- V-min bias and sum_t p on the matrix cores: A row c < CG holds the
@@ -692,15 +717,17 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) {
       const int w = (VB == 2) ? bb : (2 * bb + (r >> 3));
-      const uint32_t* src = vsp + (w * 4 + byte) * 16;
+      const int sl = L::vslot(w);
+      const uint32_t* src = vsp + sl * 64 + byte * 16;
+      const int sw = L::vswz(sl, byte);
       u4_t x;
       if constexpr (KB == 8) {
         // PV slots (2m, 2m + 1) hold the token pair 8 (m >> 1) + 2 g4 + (m & 1)
-        const u2_t x0 = *reinterpret_cast<const u2_t*>(src + 2 * g4);
-        const u2_t x1 = *reinterpret_cast<const u2_t*>(src + 8 + 2 * g4);
+        const u2_t x0 = *reinterpret_cast<const u2_t*>(src + ((2 * g4) ^ sw));
+        const u2_t x1 = *reinterpret_cast<const u2_t*>(src + ((8 + 2 * g4) ^ sw));
         x = u4_t{x0[0], x0[1], x1[0], x1[1]};
       } else {
-        x = *reinterpret_cast<const u4_t*>(src + 4 * g4);
+        x = *reinterpret_cast<const u4_t*>(src + ((4 * g4) ^ sw));
       }
       u4_t a;
 #pragma unroll
@@ -861,8 +888,8 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
     using L = StageLayout<HD, KB, VB>;
     constexpr int CG = HD / 32;
     for (int t = tid; t < kStage; t += kThreads) {
-      reinterpret_cast<uint16_t*>(buf0 + L::off_vm)[CG * kStage + t] = 0x3C00;
-      reinterpret_cast<uint16_t*>(buf1 + L::off_vm)[CG * kStage + t] = 0x3C00;
+      reinterpret_cast<uint16_t*>(buf0 + L::off_vm)[CG * L::vms + t] = 0x3C00;
+      reinterpret_cast<uint16_t*>(buf1 + L::off_vm)[CG * L::vms + t] = 0x3C00;
     }
   }
   R ra, rb;
@@ -1122,16 +1149,23 @@ decode_mfma_kernel(const DecodeParams p) {
 
 }  // namespace
 
-// LDS bytes of one stage buffer for the largest K / V bit widths of a launch
+// LDS bytes of one stage buffer: the largest layout of any (K, V) bit width
+// pair a segment of the launch can have (K up to kb, V up to vb bits)
+template <int HD>
+static int kivi_stage_bytes_hd(int kb, int vb) {
+  const int sizes[3][3] = {
+      {StageLayout<HD, 2, 2>::bytes, StageLayout<HD, 2, 4>::bytes, StageLayout<HD, 2, 8>::bytes},
+      {StageLayout<HD, 4, 2>::bytes, StageLayout<HD, 4, 4>::bytes, StageLayout<HD, 4, 8>::bytes},
+      {StageLayout<HD, 8, 2>::bytes, StageLayout<HD, 8, 4>::bytes, StageLayout<HD, 8, 8>::bytes}};
+  int best = 0;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j)
+      if ((2 << i) <= kb && (2 << j) <= vb) best = std::max(best, sizes[i][j]);
+  return best;
+}
+
 static int kivi_stage_bytes(int hd, int kb, int vb) {
-  if (hd == 128) {
-    if (kb == 8 || vb == 8) return StageLayout<128, 8, 8>::bytes;
-    if (kb == 4 || vb == 4) return StageLayout<128, 4, 4>::bytes;
-    return StageLayout<128, 2, 2>::bytes;
-  }
-  if (kb == 8 || vb == 8) return StageLayout<64, 8, 8>::bytes;
-  if (kb == 4 || vb == 4) return StageLayout<64, 4, 4>::bytes;
-  return StageLayout<64, 2, 2>::bytes;
+  return hd == 128 ? kivi_stage_bytes_hd<128>(kb, vb) : kivi_stage_bytes_hd<64>(kb, vb);
 }
 
 int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, int max_vbits,

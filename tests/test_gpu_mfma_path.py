@@ -54,6 +54,33 @@ def test_mfma_matches_generic_and_oracle(gpu, hd, kb, vb):
     np.testing.assert_allclose(fast, slow, atol=1e-3, rtol=1e-2)
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("kb,vb", [(2, 2), (2, 4), (2, 8), (4, 2), (4, 4), (4, 8), (8, 2),
+                                   (8, 4), (8, 8)])
+def test_mfma_whole_segment_in_one_chunk(gpu, hd, kb, vb):
+    """One chunk per head group: a workgroup runs all 12 stages of the segment through
+    both LDS stage buffers (prologue, steady loop, tail, ragged last stage).  The launch
+    holds only this width pair, so its stage buffers are sized for exactly this layout."""
+    from phasekv_amd import decode as dec
+    from phasekv_amd.kernels.packing import quantize_pack
+    print(f"case hd={hd} bits={kb},{vb}", flush=True)
+    g = torch.Generator().manual_seed(kb * 100 + vb + hd)
+    hq, hkv, length = 8, 2, 1500
+    q = torch.randn(1, hq, hd, generator=g).to(torch.float16)
+    kd = (torch.randn(1, hkv, length, hd, generator=g) * 2).to(torch.float16)
+    vd = torch.randn(1, hkv, length, hd, generator=g).to(torch.float16)
+    pk = quantize_pack(kd.to(gpu), kb, -2, 32)
+    pv = quantize_pack(vd.to(gpu), vb, -1, 32)
+    seg = dec.packed_segment(pk, pv, batched=True, splits=1)
+    fast = _run(q.to(gpu), [seg], hq, False)[0].float().cpu().numpy()
+    slow = _run(q.to(gpu), [seg], hq, True)[0].float().cpu().numpy()
+    deq_k = po.dequantize_float(_np_pt(pk))[0]
+    deq_v = po.dequantize_float(_np_pt(pv))[0]
+    want = ao.segments_attention(q[0].numpy(), [(deq_k, deq_v)], hq)
+    np.testing.assert_allclose(fast, want, atol=2e-3, rtol=1e-2)
+    np.testing.assert_allclose(fast, slow, atol=1e-3, rtol=1e-2)
+
+
 @pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (16, 1), (28, 4), (32, 1), (40, 2)])
 def test_mfma_gqa_groups_and_head_slabs(gpu, hq, hkv):
     from phasekv_amd import decode as dec
