@@ -194,7 +194,10 @@ struct StageLayout {
   static constexpr int vpw = (vrow_words >= 16) ? 4 : 2;
   static constexpr int vnq = vrow_words / vpw;
   static constexpr int vgrp_words = vrow_words * 64;           // spread group stride (words)
-  static constexpr int vw_bytes = vspread ? 4 * vgrp_words * 4 : kStage * vrow_bytes;
+  // 8-bit V rows padded by 16 bytes: the token rows 4 apart that one half wave
+  // reads sit 16 banks apart
+  static constexpr int vrow_pitch = vrow_bytes + 16;
+  static constexpr int vw_bytes = vspread ? 4 * vgrp_words * 4 : kStage * vrow_pitch;
   // V scale / min rows of kStage tokens, padded so the rows of the bias
   // operand read start 4 banks apart
   static constexpr int vms = kStage + 8;
@@ -488,11 +491,12 @@ __device__ __forceinline__ void store_stage(const StageRegs<HD, KB, VB>& r, bool
       }
     }
   } else {
-    u4_t* vw = reinterpret_cast<u4_t*>(st + L::off_vw);
+    constexpr int PR = L::vrow_bytes / 16;   // 16-byte pieces per row
 #pragma unroll
     for (int i = 0; i < R::NV; ++i) {
       const int q = tid + kThreads * i;
-      if (R::VP % kThreads == 0 || q < R::VP) vw[q] = r.v[i];
+      if (R::VP % kThreads == 0 || q < R::VP)
+        *reinterpret_cast<u4_t*>(st + L::off_vw + (q / PR) * L::vrow_pitch + (q % PR) * 16) = r.v[i];
     }
   }
   {
@@ -704,8 +708,7 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
     for (int m = 0; m < 4; ++m) pp[c][m] = pkmul(p2[m], sv[m]);
   }
   // ---- O^T += codes_V^T * P' : channel block b, row r <-> channel 16 b + r ----
-  constexpr int RW = L::vrow_words;
-  const char* vw = st + L::off_vw + grp * kTile * L::vrow_bytes;
+  const char* vw = st + L::off_vw + grp * kTile * L::vrow_pitch;
   int tok[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) tok[j] = pv_token<KB>(g4, j);
@@ -742,8 +745,8 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
       u4_t a;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const uint32_t wa = lds_u32(vw + (tok[2 * m] * RW + w) * 4);
-        const uint32_t wb = lds_u32(vw + (tok[2 * m + 1] * RW + w) * 4);
+        const uint32_t wa = lds_u32(vw + tok[2 * m] * L::vrow_pitch + w * 4);
+        const uint32_t wb = lds_u32(vw + tok[2 * m + 1] * L::vrow_pitch + w * 4);
         a[m] = perm(wb, wa, vsel);
       }
       acc.o[b] = mfma(a, pp[b >> 1], acc.o[b]);
