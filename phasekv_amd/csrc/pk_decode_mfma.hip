@@ -542,11 +542,12 @@ __device__ __forceinline__ int pv_slot(int h, int e) {
 // ---------------------------------------------------------------------------
 // one staged 32-token KIVI group
 // ---------------------------------------------------------------------------
-template <int HD, int KB, int VB, bool FULL>
+// L: the LDS layout (StageLayout for a workgroup stage, GroupLayout for a wave's
+// own group buffer); grp is the group within it
+template <int HD, int KB, int VB, bool FULL, typename L = StageLayout<HD, KB, VB>>
 __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, bool ktm,
                                            const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc, float sl2,
                                            int lane) {
-  using L = StageLayout<HD, KB, VB>;
   const char* kwg = st + grp * KB * L::kw_row * 4;        // the group's Kw rows
   const char* ktg = st + grp * 4 * KB * L::kt_pitch;      // the group's Kt byte rows
   const char* ksg = st + L::off_ks + grp * HD * 2;
@@ -850,21 +851,27 @@ __device__ __forceinline__ void stage_group(const char* st, int i, int t_first, 
   }
 }
 
+// Register sets of stage loads in flight: two for the small 2-bit stages, one
+// otherwise (the register budget of two workgroups per CU)
+__host__ __device__ constexpr int kivi_depth(int kb, int vb, int maxb) {
+  return (kb + vb <= 4) ? 2 : 1;
+}
+
 // Every wave of the workgroup runs this with the same arguments (the stage
-// barriers are workgroup-wide).  Stage i lives in LDS buffer i % 2; while the
-// waves compute it, the loads of the next DEPTH stages are in flight in
-// registers (stages 0, 2, 4, ... in ra, 1, 3, 5, ... in rb when DEPTH is 2).
-// FAST: the unconditional loads of load_stage_fast, in a steady-state loop
-// unrolled so that each half uses one register set; the compiler then waits
+// barriers are workgroup-wide).  Stage i lives in LDS buffer i % 2 and is
+// loaded into register set i % D; while the waves compute stage i, the loads of
+// stages i + 2 .. i + 1 + D are in flight.  The steady-state loop is unrolled D
+// times so every register set index is a constant.
+// FAST: the unconditional loads of load_stage_fast; the compiler then waits
 // only for the stage it stores.  Otherwise the general loads of load_stage.
-template <int HD, int KB, int VB, bool FAST>
+template <int HD, int KB, int VB, int MAXB, bool FAST>
 __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o,
                                             const KivLoad& kl, int t_first, int t_stride, int nst,
                                             int t_end, int wave, int lane, int tid, char* lds,
                                             int stage_bytes, const u4_t (&qb)[HD / 32],
                                             WaveAcc<HD>& acc, float sl2) {
   using R = StageRegs<HD, KB, VB>;
-  constexpr int DEPTH = (KB + VB <= 4) ? 2 : 1;
+  constexpr int D = kivi_depth(KB, VB, MAXB);
   const int t_last = t_end - 1;
   FastOffsets<HD, KB, VB> fo;
   if constexpr (FAST) {
@@ -895,67 +902,262 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
       reinterpret_cast<uint16_t*>(buf1 + L::off_vm)[CG * L::vms + t] = 0x3C00;
     }
   }
-  R ra, rb;
+  auto buf = [&](int st) { return (st & 1) ? buf1 : buf0; };
+  R r[D];
+  // stage 0 goes out alone: every workgroup starts at once, and its first
+  // stage should not queue behind everybody's next ones
+  load(r[0], 0);
+  store_stage<HD, KB, VB>(r[0], kl.kmeta_gm, kl.kdata_tm, tid, buf0);
+#pragma unroll
+  for (int k = 1; k <= D; ++k)
+    if (k < nst) load(r[k % D], k);
+  __syncthreads();
   int i = 0;
-  if constexpr (DEPTH == 2) {
-    // stage 0 goes out alone: every workgroup starts at once, and its first
-    // stage should not queue behind everybody's next ones
-    load(ra, 0);
-    store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, buf0);
-    if (nst > 1) load(rb, 1);
-    if (nst > 2) load(ra, 2);
-    __syncthreads();
-    // steady state: stages i + 1 and i + 2 in flight, i + 3 and i + 4 loaded here
-    for (; i + 4 < nst; i += 2) {
-      stage_group<HD, KB, VB>(buf0, i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb, acc, sl2);
-      store_stage<HD, KB, VB>(rb, kl.kmeta_gm, kl.kdata_tm, tid, buf1);
-      load(rb, i + 3);
-      __syncthreads();
-      stage_group<HD, KB, VB>(buf1, i + 1, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb, acc, sl2);
-      store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, buf0);
-      load(ra, i + 4);
+  // steady state: stage i + j computed, i + j + 1 stored, i + j + 1 + D loaded
+  for (; i + 2 * D < nst; i += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      stage_group<HD, KB, VB>(buf(i + j), i + j, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb,
+                              acc, sl2);
+      store_stage<HD, KB, VB>(r[(j + 1) % D], kl.kmeta_gm, kl.kdata_tm, tid, buf(i + j + 1));
+      load(r[(j + 1) % D], i + j + 1 + D);
       __syncthreads();
     }
-    // tail: at most four stages left, none loaded beyond nst
-    for (; i < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb,
-                              acc, sl2);
-      if (i + 1 < nst) {
-        if (i & 1) {
-          store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, buf0);
-          if (i + 3 < nst) load(ra, i + 3);
-        } else {
-          store_stage<HD, KB, VB>(rb, kl.kmeta_gm, kl.kdata_tm, tid, buf1);
-          if (i + 3 < nst) load(rb, i + 3);
+  }
+  // tail: at most 2 D stages left, none loaded beyond nst; one copy of the
+  // group code, the register set picked by constant index
+  for (; i < nst; ++i) {
+    stage_group<HD, KB, VB>(buf(i), i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb, acc,
+                            sl2);
+    if (i + 1 < nst) {
+      const int set = (i + 1) % D;
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        if (set == k) {
+          store_stage<HD, KB, VB>(r[k], kl.kmeta_gm, kl.kdata_tm, tid, buf(i + 1));
+          if (i + 1 + D < nst) load(r[k], i + 1 + D);
         }
-        __syncthreads();
       }
-    }
-  } else {
-    load(ra, 0);
-    store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, buf0);
-    if (nst > 1) load(ra, 1);
-    __syncthreads();
-    for (; i + 2 < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb,
-                              acc, sl2);
-      store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, (i & 1) ? buf0 : buf1);
-      load(ra, i + 2);
       __syncthreads();
     }
-    for (; i < nst; ++i) {
-      stage_group<HD, KB, VB>((i & 1) ? buf1 : buf0, i, t_first, t_stride, t_end, kl.kdata_tm, wave, lane, qb,
-                              acc, sl2);
-      if (i + 1 < nst) {
-        store_stage<HD, KB, VB>(ra, kl.kmeta_gm, kl.kdata_tm, tid, (i & 1) ? buf0 : buf1);
-        __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wave-private groups.  For token-major K codes with group-major K metadata
+// (the storage quantize_pack writes) every piece of a 32-token group is one
+// contiguous block, so each wave streams its own groups (wave, wave + 4, ...)
+// through two LDS buffers of its own and the waves of a workgroup meet only at
+// the final merge: no workgroup barrier per stage, no waiting for the slowest
+// wave.  Widths up to 4 bits (two buffers per wave fit the LDS of two
+// workgroups per CU).
+// ---------------------------------------------------------------------------
+template <int HD, int KB, int VB>
+struct GroupLayout {
+  static_assert(VB != 8, "8-bit V groups use the workgroup stages");
+  static constexpr int kw_row = HD;                       // channel-major K rows: not used
+  static constexpr int kt_pitch = HD + 8;                 // as StageLayout
+  static constexpr int off_ks = 4 * KB * kt_pitch;
+  static constexpr int off_km = off_ks + HD * 2;
+  static constexpr int off_vw = off_km + HD * 2;
+  static constexpr int vrow_words = HD * VB / 32;
+  static constexpr int vrow_bytes = HD * VB / 8;
+  static constexpr bool vspread = true;
+  static constexpr int vpw = (vrow_words >= 16) ? 4 : 2;
+  static constexpr int vnq = vrow_words / vpw;
+  static constexpr int vgrp_words = vrow_words * 64;
+  static constexpr int vrow_pitch = vrow_bytes + 16;
+  // V scale / min rows of one group's 32 tokens: 40 halves apart, so the rows
+  // of the bias operand read start 20 banks apart
+  static constexpr int vms = kTile + 8;
+  static constexpr int off_vs = off_vw + vgrp_words * 4;
+  static constexpr int off_vm = off_vs + (HD / 32) * vms * 2;
+  static constexpr int bytes = (off_vm + (HD / 32 + 1) * vms * 2 + 15) & ~15;
+  __device__ static constexpr int vslot(int w) { return (w % vpw) * vnq + w / vpw; }
+  __device__ static constexpr int vswz(int s, int b) { return 8 * ((s ^ (b >> 1)) & 1); }
+};
+
+// One lane's share of a group's loads (64 lanes).
+template <int HD, int KB, int VB>
+struct GroupRegs {
+  static constexpr int KP = 4 * KB * HD / 16;   // 16-byte K pieces (4 KB byte rows of HD)
+  static constexpr int NK = (KP + 63) / 64;
+  static constexpr int W = HD * VB / 32;        // words per V row
+  static constexpr int PW = (W >= 16) ? 4 : 2;
+  static constexpr int NQ = W / PW;
+  static constexpr int VI = 16 * NQ;            // V items (token pair, slice) of a group
+  u4_t k[NK];
+  u4_t va, vb;
+  u2_t km;     // lanes < HD / 2: 4 channels of the group's K scales (lane < HD / 4) or mins
+  u2_t vm;     // V scales (lanes < 32) or mins of token lane % 32 (HD = 64: low word only)
+};
+
+// Loads of the group at token t0 (a multiple of 32 from the segment start); every
+// lane loads unconditionally, addresses clamped into the segment.
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void load_group(GroupRegs<HD, KB, VB>& r, const SegDev& s,
+                                           const SegOffsets& o, const KivLoad& kl, int t0,
+                                           int t_last, int lane) {
+  using R = GroupRegs<HD, KB, VB>;
+  const uint32_t row0 = (uint32_t)t0 * KB / 8;
+  const uint32_t last = (uint32_t)((kl.k_rows - row0) * (HD / 16)) - 1u;
+  const uint8_t* kbase = s.kd + o.kd + (int64_t)row0 * HD;
+#pragma unroll
+  for (int i = 0; i < R::NK; ++i) {
+    const uint32_t q = min((uint32_t)(lane + 64 * i), (uint32_t)R::KP - 1u);
+    r.k[i] = *reinterpret_cast<const u4_t*>(kbase + 16u * min(q, last));
+  }
+  {
+    constexpr int QL = HD / 4;    // lanes per tensor, 4 channels each
+    const int q = lane & (2 * QL - 1);
+    const uint16_t* m = pick(q < QL, s.ks, s.km) + o.km + (int64_t)(t0 / kTile) * HD + 4 * (q & (QL - 1));
+    r.km = *reinterpret_cast<const u2_t*>(m);
+  }
+  {
+    constexpr int RB = HD * VB / 8;
+    const int q = lane % R::VI;
+    const int tp = q / R::NQ, qw = q - tp * R::NQ;
+    const int ta = min(t0 + 2 * tp, t_last), tb = min(t0 + 2 * tp + 1, t_last);
+    const uint8_t* vseg = s.vd + o.vd;
+    const uint8_t* pa = vseg + (int64_t)ta * RB + qw * R::PW * 4;
+    const uint8_t* pb = vseg + (int64_t)tb * RB + qw * R::PW * 4;
+    if constexpr (R::PW == 4) {
+      r.va = *reinterpret_cast<const u4_t*>(pa);
+      r.vb = *reinterpret_cast<const u4_t*>(pb);
+    } else {
+      const u2_t a = *reinterpret_cast<const u2_t*>(pa);
+      const u2_t b = *reinterpret_cast<const u2_t*>(pb);
+      r.va = u4_t{a[0], a[1], 0u, 0u};
+      r.vb = u4_t{b[0], b[1], 0u, 0u};
+    }
+  }
+  {
+    const int t = min(t0 + (lane & (kTile - 1)), t_last);
+    const uint16_t* m = pick(lane < kTile, s.vs, s.vm) + o.vm + (int64_t)t * (HD / 32);
+    if (HD == 128) r.vm = *reinterpret_cast<const u2_t*>(m);
+    else r.vm = u2_t{*reinterpret_cast<const uint32_t*>(m), 0u};
+  }
+}
+
+// The group's registers into the wave's buffer (GroupLayout).
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void store_group(const GroupRegs<HD, KB, VB>& r, int lane, char* st) {
+  using L = GroupLayout<HD, KB, VB>;
+  using R = GroupRegs<HD, KB, VB>;
+#pragma unroll
+  for (int i = 0; i < R::NK; ++i) {
+    const int q = lane + 64 * i;
+    if (R::KP % 64 == 0 || q < R::KP) {
+      u2_t* dst = reinterpret_cast<u2_t*>(st + (q / (HD / 16)) * L::kt_pitch + (q % (HD / 16)) * 16);
+      dst[0] = u2_t{r.k[i][0], r.k[i][1]};
+      dst[1] = u2_t{r.k[i][2], r.k[i][3]};
+    }
+  }
+  {
+    constexpr int QL = HD / 4;
+    if (lane < 2 * QL) {
+      uint16_t* m = reinterpret_cast<uint16_t*>(st + ((lane < QL) ? L::off_ks : L::off_km));
+      *reinterpret_cast<u2_t*>(m + 4 * (lane & (QL - 1))) = r.km;
+    }
+  }
+  if (R::VI == 64 || lane < R::VI) {
+    // the store order of StageLayout: 32 stores of a half wave in 32 banks
+    const int tp = lane / R::NQ, qw = lane - tp * R::NQ;
+    const int flip = ((R::NQ == 4) ? (qw >> 1) : qw) & 1;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(st + L::off_vw) + qw * 64;
+#pragma unroll
+    for (int k = 0; k < R::PW; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int b = j ^ flip;
+        const int sw = 8 * ((qw ^ (j >> 1)) & 1);
+        dst[k * R::NQ * 64 + b * 16 + (tp ^ sw)] = perm(r.vb[k], r.va[k], sel_bytes(b));
       }
+  }
+  {
+    uint16_t* m = reinterpret_cast<uint16_t*>(st + ((lane < kTile) ? L::off_vs : L::off_vm));
+    const int t = lane & (kTile - 1);
+#pragma unroll
+    for (int cg = 0; cg < HD / 32; ++cg)
+      m[cg * L::vms + t] = (uint16_t)(r.vm[cg >> 1] >> (16 * (cg & 1)));
+  }
+}
+
+// LDS written by the lanes of a wave, then read by other lanes of the same wave:
+// a wave's LDS operations run in order, so only the compiler must not move them
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The wave's groups of the chunk [t_first, t_end): group i at t_first + 32 (wave + 4 i),
+// in buffer i % 2 of the wave, loaded into register set i % D.
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void kivi_wave_groups(const SegDev& s, const SegOffsets& o,
+                                                 const KivLoad& kl, int t_first, int t_end,
+                                                 int wave, int lane, char* lds,
+                                                 const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
+                                                 float sl2) {
+  using L = GroupLayout<HD, KB, VB>;
+  using R = GroupRegs<HD, KB, VB>;
+  constexpr int D = (KB + VB <= 4) ? 2 : 1;
+  constexpr int CG = HD / 32;
+  const int ng = (t_end - t_first + kTile - 1) / kTile;
+  const int n = (ng - wave + kWaves - 1) / kWaves;
+  if (n <= 0) return;
+  const int t_last = t_end - 1;
+  char* b0 = lds + wave * 2 * L::bytes;
+  char* b1 = b0 + L::bytes;
+  // the ones row of both buffers' V-min block (never overwritten by the groups)
+  if (lane < kTile) {
+    reinterpret_cast<uint16_t*>(b0 + L::off_vm)[CG * L::vms + lane] = 0x3C00;
+    reinterpret_cast<uint16_t*>(b1 + L::off_vm)[CG * L::vms + lane] = 0x3C00;
+  }
+  auto tok = [&](int i) { return t_first + kTile * (wave + kWaves * i); };
+  auto buf = [&](int i) { return (i & 1) ? b1 : b0; };
+  auto load = [&](R& r, int i) { load_group<HD, KB, VB>(r, s, o, kl, tok(i), t_last, lane); };
+  auto group = [&](int i) {
+    const int nvalid = min(kTile, t_end - tok(i));
+    if (nvalid == kTile) kivi_group<HD, KB, VB, true, L>(nvalid, buf(i), 0, true, qb, acc, sl2, lane);
+    else kivi_group<HD, KB, VB, false, L>(nvalid, buf(i), 0, true, qb, acc, sl2, lane);
+  };
+  R r[D];
+  // group 0 goes out alone, then groups 1 .. D
+  load(r[0], 0);
+  store_group<HD, KB, VB>(r[0], lane, b0);
+#pragma unroll
+  for (int k = 1; k <= D; ++k)
+    if (k < n) load(r[k % D], k);
+  wave_lds_sync();
+  int i = 0;
+  for (; i + 2 * D < n; i += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      group(i + j);
+      store_group<HD, KB, VB>(r[(j + 1) % D], lane, buf(i + j + 1));
+      load(r[(j + 1) % D], i + j + 1 + D);
+      wave_lds_sync();
+    }
+  }
+  for (; i < n; ++i) {
+    group(i);
+    if (i + 1 < n) {
+      const int set = (i + 1) % D;
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        if (set == k) {
+          store_group<HD, KB, VB>(r[k], lane, buf(i + 1));
+          if (i + 1 + D < n) load(r[k], i + 1 + D);
+        }
+      }
+      wave_lds_sync();
     }
   }
 }
 
 // Stages of the chunk: t_first + i t_stride (i < nst), tokens below t_end.
-template <int HD, int KB, int VB>
+template <int HD, int KB, int VB, int MAXB>
 __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_first,
                                            int t_stride, int nst, int t_end, int wave, int lane,
                                            int tid, char* lds, int stage_bytes,
@@ -979,11 +1181,17 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
   kl.gm_elems = s.kmeta_gm && !meta8;
   kl.kmeta4 = !s.kmeta_gm && (kl.row_groups % 4 == 0) && (t_first % kStage == 0) &&
               (t_stride % kStage == 0) && meta8;
+  if constexpr (KB <= 4 && VB <= 4) {
+    if (kl.kdata_tm && kl.kmeta_gm && kl.row_bytes < ((int64_t)1 << 31) / HD) {
+      kivi_wave_groups<HD, KB, VB>(s, o, kl, t_first, t_end, wave, lane, lds, qb, acc, sl2);
+      return;
+    }
+  }
   if (kl.kmode == 16 && (kl.kmeta4 || kl.kmeta_gm) && kl.row_bytes < ((int64_t)1 << 31) / HD)
-    kivi_stages<HD, KB, VB, true>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
+    kivi_stages<HD, KB, VB, MAXB, true>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
                                   stage_bytes, qb, acc, sl2);
   else
-    kivi_stages<HD, KB, VB, false>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
+    kivi_stages<HD, KB, VB, MAXB, false>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
                                    stage_bytes, qb, acc, sl2);
 }
 
@@ -1059,7 +1267,7 @@ decode_mfma_kernel(const DecodeParams p) {
 #define PK_KIVI_CASE(KB_, VB_)                                                                 \
   if constexpr (KB_ <= MAXB && VB_ <= MAXB) {                                                  \
     if (knst > 0 && s.kbits == KB_ && s.vbits == VB_)                                          \
-      kivi_chunk<HD, KB_, VB_>(s, o, kt_first, kt_stride, knst, kt_end, wave, lane, tid, lds,  \
+      kivi_chunk<HD, KB_, VB_, MAXB>(s, o, kt_first, kt_stride, knst, kt_end, wave, lane, tid, lds,  \
                                p.stage_lds, qb, acc, sl2);                                     \
   }
     PK_KIVI_CASE(2, 2) PK_KIVI_CASE(2, 4) PK_KIVI_CASE(2, 8)
@@ -1167,6 +1375,22 @@ static int kivi_stage_bytes_hd(int kb, int vb) {
   return best;
 }
 
+// LDS bytes of one wave's group buffer (widths up to 4 bits; 0 if none fit)
+template <int HD>
+static int kivi_group_bytes_hd(int kb, int vb) {
+  const int sizes[2][2] = {{GroupLayout<HD, 2, 2>::bytes, GroupLayout<HD, 2, 4>::bytes},
+                           {GroupLayout<HD, 4, 2>::bytes, GroupLayout<HD, 4, 4>::bytes}};
+  int best = 0;
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j)
+      if ((2 << i) <= kb && (2 << j) <= vb) best = std::max(best, sizes[i][j]);
+  return best;
+}
+
+static int kivi_group_bytes(int hd, int kb, int vb) {
+  return hd == 128 ? kivi_group_bytes_hd<128>(kb, vb) : kivi_group_bytes_hd<64>(kb, vb);
+}
+
 static int kivi_stage_bytes(int hd, int kb, int vb) {
   return hd == 128 ? kivi_stage_bytes_hd<128>(kb, vb) : kivi_stage_bytes_hd<64>(kb, vb);
 }
@@ -1176,7 +1400,8 @@ int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, in
   DecodeParams dp = dp_in;
   const int hd = dp.hd;
   dp.stage_lds = (kivi_stage_bytes(hd, max_kbits, max_vbits) + 15) & ~15;
-  const size_t staging = 2 * (size_t)dp.stage_lds;
+  const size_t staging = std::max(2 * (size_t)dp.stage_lds,
+                                  (size_t)kWaves * 2 * kivi_group_bytes(hd, max_kbits, max_vbits));
   const size_t merge = sizeof(float) * ((size_t)kWaves * 16 * (hd + 4) + 2 * kWaves * 16);
   const size_t lds = std::max(staging, merge);
   dim3 grid(lchunks, dp.Hkv * dp.nslab, dp.B);
