@@ -37,6 +37,23 @@ __device__ inline Block3 xcd_block() {
   return o;
 }
 
+// Chunk-major order: the hardware dispatches workgroups in linear order, so with
+// the chunk index varying slowest every row's chunk 0 goes out first.  The host
+// numbers the costliest chunks first, so that workgroups beyond the resident
+// capacity are the cheap ones.  (No XCD grouping: with token-major K and
+// group-major metadata neighbouring chunks share no lines.)
+__device__ inline Block3 chunk_major_block() {
+  const uint32_t gx = gridDim.x, gy = gridDim.y;
+  const uint32_t rows = gy * gridDim.z;
+  const uint32_t lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const uint32_t r = lin % rows;
+  Block3 o;
+  o.x = (int)(lin / rows);
+  o.y = (int)(r % gy);
+  o.z = (int)(r / gy);
+  return o;
+}
+
 // One segment as the kernels see it (element strides, see pk_segment).
 struct SegDev {
   int kind, length, kbits, vbits, kgs, vgs;
@@ -68,6 +85,7 @@ struct DecodeParams {
   int C;              // chunks per (batch, kv head) over all segments
   int nseg;
   int stage_lds;      // MFMA kernel: LDS bytes of one stage buffer (two are used)
+  int order;          // MFMA kernel: 1 = chunk-major workgroup order, 0 = grouped by XCD
   SegDev seg[kMaxSeg];
 };
 

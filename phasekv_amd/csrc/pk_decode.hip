@@ -337,6 +337,8 @@ struct Plan {
   int C;
   int max_kbits, max_vbits;
   std::vector<int> n_chunks, chunk_len, gbegin;
+  std::vector<int> seg_order;   // launch order of the segments (costliest chunks first)
+  int order = 0;                // MFMA kernel workgroup order (DecodeParams::order)
   size_t off_m, off_l, off_acc, bytes;
 };
 
@@ -390,6 +392,108 @@ static int64_t env_int(const char* name, int64_t dflt) {
   return std::max<int64_t>(1, atoll(v));
 }
 
+// Relative cost of a 32-token group in the MFMA kernel (measured on MI355X at
+// batch 8, hd 128): 2/2-bit 100, 4/4-bit 118, 2/8-bit 150, 8/8-bit 190, fp16 280.
+static int group_weight(const pk_segment& s) {
+  if (s.kind == PK_SEG_FP16) return 280;
+  const int lo = std::min(s.k_bits, s.v_bits), hi = std::max(s.k_bits, s.v_bits);
+  if (hi == 2) return 100;
+  if (hi == 4) return lo == 2 ? 110 : 118;
+  return lo == 2 ? 150 : lo == 4 ? 165 : 190;
+}
+
+// Automatic plan of the MFMA kernel: per-segment chunk lengths (whole 32-token
+// groups, at least one per wave) sized by group weight, so every chunk costs about the same whatever its segment's bit
+// widths, and the number of chunks per row chosen among a few candidates around
+// one and two workgroups per CU by an estimate of the finishing time (fitted to
+// MI355X measurements): chunk cost = 5 + groups per wave * weight * t, t = 1
+// alone on a CU and 1.8 with a second workgroup; workgroups beyond two per CU run
+// as the cheapest chunks (launch order), so they add about half a cheap chunk.
+static void plan_weighted(const pk_decode_problem* p, int64_t per_bh, Plan& pl) {
+  const int ns = p->num_segments;
+  std::vector<int64_t> G(ns), w(ns);
+  int64_t row = 0;
+  for (int i = 0; i < ns; ++i) {
+    G[i] = cdiv(p->segments[i].length, 32);
+    w[i] = group_weight(p->segments[i]);
+    row += G[i] * w[i];
+  }
+  const int64_t cus = device_cu_count(), slots = 2 * cus;
+  std::vector<int64_t> g(ns), best_g(ns, 4);
+  double best = 1e30;
+  int64_t best_wgs = 0;
+  auto evaluate = [&](int64_t U) -> int64_t {   // plan for chunk cost U; returns workgroups
+    int64_t wgs = 0;
+    for (int i = 0; i < ns; ++i) {
+      g[i] = std::min(G[i], std::max<int64_t>(4, U / w[i]));
+      wgs += cdiv(G[i], g[i]) * per_bh;
+    }
+    const double t = wgs <= cus ? 1.0 : 1.8;
+    auto cost = [&](int64_t groups, int64_t wi) {
+      return 5.0 + std::ceil(groups / 4.0) * (double)wi / 100.0 * t;
+    };
+    double cmax = 0, cmin = 1e30, total = 0;
+    for (int i = 0; i < ns; ++i) {
+      const int64_t n = cdiv(G[i], g[i]);
+      const double c = cost(g[i], w[i]);
+      cmax = std::max(cmax, c);
+      cmin = std::min(cmin, c);
+      total += ((double)(n - 1) * c + cost(G[i] - (n - 1) * g[i], w[i])) * (double)per_bh;
+    }
+    const double est = wgs <= slots ? cmax : std::max(cmax, total / slots) + 0.5 * cmin;
+    if (est < best - 1e-9 || (est < best + 1e-9 && wgs < best_wgs)) {
+      best = est;
+      best_wgs = wgs;
+      best_g = g;
+    }
+    return wgs;
+  };
+  const int64_t forced = env_int("PK_PLAN_UNITS", 0);   // a fixed chunk cost, for experiments
+  if (forced > 0) {
+    best = 1e30;
+    evaluate(forced);
+    best = -1.0;   // keep it
+  }
+  // the smallest chunks that fit one, then two workgroups per CU
+  for (int64_t cap : {cus, slots}) {
+    int64_t U = std::max<int64_t>(400, cdiv(row * per_bh, cap));
+    for (int it = 0; it < 64 && evaluate(U) > cap; ++it) U += std::max<int64_t>(1, U / 32);
+  }
+  // and a few with more workgroups than two per CU
+  for (double f : {1.25, 1.5, 2.0, 3.0})
+    evaluate(std::max<int64_t>(400, (int64_t)(row * per_bh / (f * slots))));
+  std::vector<double> cost(ns);
+  for (int i = 0; i < ns; ++i) {
+    pl.chunk_len.push_back(static_cast<int>(std::min<int64_t>(32 * best_g[i], p->segments[i].length)));
+    pl.n_chunks.push_back(static_cast<int>(cdiv(G[i], best_g[i])));
+    pl.gbegin.push_back(pl.C);
+    pl.C += pl.n_chunks.back();
+    cost[i] = (double)best_g[i] * (double)w[i];
+  }
+  pl.seg_order.resize(ns);
+  for (int i = 0; i < ns; ++i) pl.seg_order[i] = i;
+  std::stable_sort(pl.seg_order.begin(), pl.seg_order.end(),
+                   [&](int a, int b) { return cost[a] > cost[b]; });
+  // chunk-major order unless a segment keeps the reference's channel-major K,
+  // whose neighbouring chunks share lines (those go to one XCD's L2)
+  pl.order = 1;
+  for (int i = 0; i < ns; ++i) {
+    const pk_segment& s = p->segments[i];
+    if (s.kind == PK_SEG_KIVI &&
+        (s.k_data_layout != PK_CODES_TOKEN_MAJOR || s.k_meta_layout != PK_META_GROUP_MAJOR))
+      pl.order = 0;
+  }
+}
+
+static bool weighted_plan(const pk_decode_problem* p) {
+  if (env_int("PK_CHUNK_TOKENS", 0) > 0 || env_int("PK_TARGET_WORKGROUPS", 0) > 0) return false;
+  const char* v = getenv("PK_WEIGHTED_PLAN");
+  if (v && v[0] == '0') return false;
+  for (int i = 0; i < p->num_segments; ++i)
+    if (p->segments[i].splits > 0) return false;
+  return true;
+}
+
 static Plan make_plan(const pk_decode_problem* p) {
   Plan pl{};
   const int hd = p->head_dim;
@@ -425,6 +529,9 @@ static Plan make_plan(const pk_decode_problem* p) {
     auto_len = std::max<int64_t>(kMinChunk, cdiv(auto_len, kMinChunk) * kMinChunk);
   }
   pl.C = 0;
+  if (pl.mfma && weighted_plan(p)) {
+    plan_weighted(p, per_bh, pl);
+  } else
   for (int i = 0; i < p->num_segments; ++i) {
     const pk_segment& s = p->segments[i];
     int64_t cl;
@@ -444,6 +551,8 @@ static Plan make_plan(const pk_decode_problem* p) {
     pl.gbegin.push_back(pl.C);
     pl.C += static_cast<int>(nc);
   }
+  if (pl.seg_order.empty())
+    for (int i = 0; i < p->num_segments; ++i) pl.seg_order.push_back(i);
   const int64_t rows = (int64_t)p->batch * p->num_q_heads;
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   pl.off_m = 0;
@@ -505,16 +614,18 @@ static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
     const int n = std::min(kMaxSeg, p->num_segments - first);
     int lchunks = 0;
     for (int i = 0; i < n; ++i) {
+      const int si = pl.seg_order[first + i];
       SegDev& d = dp.seg[i];
-      fill_segment(d, p->segments[first + i]);
+      fill_segment(d, p->segments[si]);
       d.hd_meta = p->head_dim;
-      d.chunk_len = pl.chunk_len[first + i];
-      d.n_chunks = pl.n_chunks[first + i];
-      d.gbegin = pl.gbegin[first + i];
+      d.chunk_len = pl.chunk_len[si];
+      d.n_chunks = pl.n_chunks[si];
+      d.gbegin = pl.gbegin[si];
       d.lbegin = lchunks;
       lchunks += d.n_chunks;
     }
     dp.nseg = n;
+    dp.order = pl.order;
     int rc;
     if (pl.mfma) {
       rc = launch_decode_mfma(dp, lchunks, pl.max_kbits, pl.max_vbits, stream);

@@ -1195,6 +1195,25 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
                                    stage_bytes, qb, acc, sl2);
 }
 
+// Every 64-byte line of the argument block read at once, at entry.  The fields a
+// workgroup needs (header, segment table, launch sizes) are spread over about 25
+// lines; read where they are used, each new line is a dependent scalar-cache
+// miss.  Afterwards those loads hit.
+__device__ __forceinline__ void touch_params(const DecodeParams& p) {
+  constexpr int kWords = (int)(sizeof(DecodeParams) / 4);
+  static_assert(kWords <= 26 * 16, "argument block above 26 lines");
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(&p);
+  // one statement consumes every value: all 26 loads are in flight together
+  asm volatile("" ::
+               "s"(w[min(0, kWords - 1)]), "s"(w[min(16, kWords - 1)]), "s"(w[min(32, kWords - 1)]), "s"(w[min(48, kWords - 1)]),
+               "s"(w[min(64, kWords - 1)]), "s"(w[min(80, kWords - 1)]), "s"(w[min(96, kWords - 1)]), "s"(w[min(112, kWords - 1)]),
+               "s"(w[min(128, kWords - 1)]), "s"(w[min(144, kWords - 1)]), "s"(w[min(160, kWords - 1)]), "s"(w[min(176, kWords - 1)]),
+               "s"(w[min(192, kWords - 1)]), "s"(w[min(208, kWords - 1)]), "s"(w[min(224, kWords - 1)]), "s"(w[min(240, kWords - 1)]),
+               "s"(w[min(256, kWords - 1)]), "s"(w[min(272, kWords - 1)]), "s"(w[min(288, kWords - 1)]), "s"(w[min(304, kWords - 1)]),
+               "s"(w[min(320, kWords - 1)]), "s"(w[min(336, kWords - 1)]), "s"(w[min(352, kWords - 1)]), "s"(w[min(368, kWords - 1)]),
+               "s"(w[min(384, kWords - 1)]), "s"(w[min(400, kWords - 1)]));
+}
+
 // Two workgroups (8 waves) per CU: the register budget is capped so a second
 // wave per SIMD hides LDS and dependency latency.
 template <int HD, int MAXB>
@@ -1209,19 +1228,26 @@ decode_mfma_kernel(const DecodeParams p) {
   const int n = lane & 15;
   const int g4 = lane >> 4;
 
-  const Block3 blk = xcd_block();
+  touch_params(p);
+  const Block3 blk = p.order ? chunk_major_block() : xcd_block();
   const int b = blk.z;
   const int kvh = blk.y / p.nslab;
   const int slab = blk.y - kvh * p.nslab;
   const int h0 = kvh * p.G + slab * p.HS;
   const int nh = min(p.HS, p.G - slab * p.HS);
 
-  int si = 0;
-  while (si + 1 < p.nseg && blk.x >= p.seg[si + 1].lbegin) ++si;
   // a register copy: fields read inside the group loop must not be reloaded
   // from the argument block (such a reload would sit in the in-order memory
-  // counter behind the prefetched group and stall on it)
-  const SegDev s = p.seg[si];
+  // counter behind the prefetched group and stall on it).  Segment 0 is read
+  // before the segment is known: the host lists the segment with the costliest
+  // (usually the most) chunks first, so most workgroups save one dependent round
+  // trip.
+  SegDev s = p.seg[0];
+  if (p.nseg > 1 && blk.x >= p.seg[1].lbegin) {
+    int si = 1;
+    while (si + 1 < p.nseg && blk.x >= p.seg[si + 1].lbegin) ++si;
+    s = p.seg[si];
+  }
   const int local = blk.x - s.lbegin;
   const int cg = s.gbegin + local;
   int len_b = s.length;
