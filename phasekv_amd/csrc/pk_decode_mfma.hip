@@ -996,9 +996,12 @@ struct GroupRegs {
 // lane loads unconditionally, addresses clamped into the segment.
 template <int HD, int KB, int VB>
 __device__ __forceinline__ void load_group(GroupRegs<HD, KB, VB>& r, const SegDev& s,
-                                           const SegOffsets& o, const KivLoad& kl, int t0,
+                                           const SegOffsets& o, const KivLoad& kl, int t0_,
                                            int t_last, int lane) {
   using R = GroupRegs<HD, KB, VB>;
+  // t0 is the same on every lane of the wave: each load below is a scalar base
+  // plus a 32-bit lane offset (no 64-bit address arithmetic per lane)
+  const int t0 = __builtin_amdgcn_readfirstlane(t0_);
   const uint32_t row0 = (uint32_t)t0 * KB / 8;
   const uint32_t last = (uint32_t)((kl.k_rows - row0) * (HD / 16)) - 1u;
   const uint8_t* kbase = s.kd + o.kd + (int64_t)row0 * HD;
@@ -1010,17 +1013,18 @@ __device__ __forceinline__ void load_group(GroupRegs<HD, KB, VB>& r, const SegDe
   {
     constexpr int QL = HD / 4;    // lanes per tensor, 4 channels each
     const int q = lane & (2 * QL - 1);
-    const uint16_t* m = pick(q < QL, s.ks, s.km) + o.km + (int64_t)(t0 / kTile) * HD + 4 * (q & (QL - 1));
+    const int64_t mrow = o.km + (int64_t)(t0 / kTile) * HD;
+    const uint16_t* m = pick(q < QL, s.ks, s.km) + mrow + 4 * (q & (QL - 1));
     r.km = *reinterpret_cast<const u2_t*>(m);
   }
   {
     constexpr int RB = HD * VB / 8;
     const int q = lane % R::VI;
-    const int tp = q / R::NQ, qw = q - tp * R::NQ;
-    const int ta = min(t0 + 2 * tp, t_last), tb = min(t0 + 2 * tp + 1, t_last);
-    const uint8_t* vseg = s.vd + o.vd;
-    const uint8_t* pa = vseg + (int64_t)ta * RB + qw * R::PW * 4;
-    const uint8_t* pb = vseg + (int64_t)tb * RB + qw * R::PW * 4;
+    const uint32_t tp = q / R::NQ, qw = q - tp * R::NQ;
+    const uint32_t dt = (uint32_t)(t_last - t0);
+    const uint8_t* vrow = s.vd + o.vd + (int64_t)t0 * RB;
+    const uint8_t* pa = vrow + (min(2u * tp, dt) * RB + qw * R::PW * 4);
+    const uint8_t* pb = vrow + (min(2u * tp + 1u, dt) * RB + qw * R::PW * 4);
     if constexpr (R::PW == 4) {
       r.va = *reinterpret_cast<const u4_t*>(pa);
       r.vb = *reinterpret_cast<const u4_t*>(pb);
@@ -1032,8 +1036,8 @@ __device__ __forceinline__ void load_group(GroupRegs<HD, KB, VB>& r, const SegDe
     }
   }
   {
-    const int t = min(t0 + (lane & (kTile - 1)), t_last);
-    const uint16_t* m = pick(lane < kTile, s.vs, s.vm) + o.vm + (int64_t)t * (HD / 32);
+    const uint32_t dt = min((uint32_t)(lane & (kTile - 1)), (uint32_t)(t_last - t0));
+    const uint16_t* m = pick(lane < kTile, s.vs, s.vm) + (o.vm + (int64_t)t0 * (HD / 32)) + dt * (HD / 32);
     if (HD == 128) r.vm = *reinterpret_cast<const u2_t*>(m);
     else r.vm = u2_t{*reinterpret_cast<const uint32_t*>(m), 0u};
   }
