@@ -107,6 +107,43 @@ def test_prefill_pack_block_full_size(gpu):
     assert torch.equal(packing.pack_low_bits(codes, 2), pk.packed)
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_fast_path_rounding_ties_bit_exact(gpu, bits):
+    """Rounding ties in the fp16 group-of-32 kernels: groups whose values sit exactly on
+    k + 1/2 scales (scale 1 and 0.5 with half-integer values at several offsets, fp16
+    values spaced 1/64 apart over random ranges) round half to even exactly as the
+    reference's round() does."""
+    from phasekv_amd.kernels.packing import quantize_pack
+    g = torch.Generator().manual_seed(bits)
+    qmax = (1 << bits) - 1
+    rows = []
+    for step in (1.0, 0.5):
+        # min = offset, max = offset + qmax * step: scale = step, and values
+        # offset + (k + 1/2) * step are exact ties (offset 0 takes the exact
+        # statistics path, the others the fast one)
+        grid = torch.arange(0, 2 * qmax + 1, dtype=torch.float32) * (step / 2)
+        for offset in (0.0, 4.0, -8.0, 64.0):
+            for _ in range(16):
+                vals = grid[torch.randint(0, grid.numel(), (32,), generator=g)]
+                vals[0], vals[1] = 0.0, qmax * step
+                rows.append(vals + offset)
+    for _ in range(128):
+        lo = float(torch.randint(-64, 64, (1,), generator=g)) / 8
+        span = float(torch.randint(1, 512, (1,), generator=g)) / 64
+        vals = lo + torch.randint(0, int(span * 64) + 1, (32,), generator=g).float() / 64
+        rows.append(vals)
+    x = torch.stack(rows).to(torch.float16)                       # [R, 32] groups
+    n = x.shape[0] // 4 * 4
+    block = x[:n].reshape(1, n // 4, 4, 32).permute(0, 2, 1, 3).reshape(1, 4, n // 4 * 32 // 32, 32)
+    for axis, data in ((-1, x[:n].reshape(1, 4, n // 4, 32)),           # V: groups along head_dim
+                       (-2, block.transpose(-1, -2).contiguous())):    # K: groups along tokens
+        pt = quantize_pack(data.to(gpu), bits, axis, 32)
+        ref = po.quantize_pack(data.numpy(), bits, axis, 32)
+        assert np.array_equal(pt.packed.cpu().numpy(), ref.packed), axis
+        assert np.array_equal(_u16(pt.scale), ref.scale.view(np.int16)), axis
+        assert np.array_equal(_u16(pt.mins), ref.mins.view(np.int16)), axis
+
+
 def test_errors_are_value_errors(gpu):
     from phasekv_amd.kernels import packing
     x = torch.zeros(1, 2, 8, 8, dtype=torch.float16, device=gpu)
