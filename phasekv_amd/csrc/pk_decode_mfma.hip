@@ -540,23 +540,26 @@ __device__ __forceinline__ int pv_slot(int h, int e) {
 }
 
 // ---------------------------------------------------------------------------
-// one staged 32-token KIVI group
+// one staged 32-token KIVI group, in two phases: kivi_qk reads the group's K
+// codes and K scale / min rows, kivi_softmax_pv its V codes and V scale / min
+// rows, so a wave can run the QK phase of its next group before the softmax
+// and PV phase of the current one
 // ---------------------------------------------------------------------------
-// L: the LDS layout (StageLayout for a workgroup stage, GroupLayout for a wave's
-// own group buffer); grp is the group within it
-template <int HD, int KB, int VB, bool FULL, typename L = StageLayout<HD, KB, VB>>
-__device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, bool ktm,
-                                           const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc, float sl2,
-                                           int lane) {
+// QK phase result: the raw S^T accumulators of instances h = 0, 1 (codes times
+// q', before the position and score factors) and the K-min bias in log2 units.
+struct QkOut {
+  f4_t d[2];
+  float bias;
+};
+
+template <int HD, int KB, typename L>
+__device__ __forceinline__ QkOut kivi_qk(const char* st, int grp, bool ktm,
+                                         const u4_t (&qb)[HD / 32], float sl2, int lane) {
   const char* kwg = st + grp * KB * L::kw_row * 4;        // the group's Kw rows
   const char* ktg = st + grp * 4 * KB * L::kt_pitch;      // the group's Kt byte rows
   const char* ksg = st + L::off_ks + grp * HD * 2;
   const char* kmg = st + L::off_km + grp * HD * 2;
-  const char* vsg = st + L::off_vs + grp * kTile * 2;     // channel group stride vms
-  const char* vmg = st + L::off_vm + grp * kTile * 2;
   constexpr int KS = HD / 32;
-  constexpr int NB = HD / 16;
-  constexpr int CG = HD / 32;
   const int r = lane & 15;     // A row (token row) / B column (head)
   const int g4 = lane >> 4;
   // ---- q folded with the group's K scale; the K-min bias sum_c q mK on the
@@ -659,6 +662,22 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
       }
     }
   }
+  return QkOut{{d[0], d[1]}, bias};
+}
+
+// Online softmax of one group's scores and O^T += codes_V^T * (p * sV) + the
+// V-min bias, from the group's V codes and V scale / min rows in LDS.
+template <int HD, int KB, int VB, bool FULL, typename L>
+__device__ __forceinline__ void kivi_softmax_pv(const QkOut& qk, int nvalid, const char* st,
+                                                int grp, WaveAcc<HD>& acc, float sl2, int lane) {
+  const char* vsg = st + L::off_vs + grp * kTile * 2;     // channel group stride vms
+  const char* vmg = st + L::off_vm + grp * kTile * 2;
+  constexpr int NB = HD / 16;
+  constexpr int CG = HD / 32;
+  const int r = lane & 15;
+  const int g4 = lane >> 4;
+  const f4_t (&d)[2] = qk.d;
+  const float bias = qk.bias;
   // ---- scores (log2 units) ----
   float sc[2][4];
   float mt = -INFINITY;
@@ -753,6 +772,16 @@ __device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, 
       acc.o[b] = mfma(a, pp[b >> 1], acc.o[b]);
     }
   }
+}
+
+// One staged 32-token KIVI group.  L: the LDS layout (StageLayout for a workgroup
+// stage, GroupLayout for a wave's own group buffer); grp is the group within it.
+template <int HD, int KB, int VB, bool FULL, typename L = StageLayout<HD, KB, VB>>
+__device__ __forceinline__ void kivi_group(int nvalid, const char* st, int grp, bool ktm,
+                                           const u4_t (&qb)[HD / 32], WaveAcc<HD>& acc, float sl2,
+                                           int lane) {
+  const QkOut qk = kivi_qk<HD, KB, L>(st, grp, ktm, qb, sl2, lane);
+  kivi_softmax_pv<HD, KB, VB, FULL, L>(qk, nvalid, st, grp, acc, sl2, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1095,8 +1124,21 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Waves with at least this many groups of a two-register-set (2-bit K and V)
+// segment run the pipelined group loop.
+constexpr int kPipeMinGroups = 8;
+
 // The wave's groups of the chunk [t_first, t_end): group i at t_first + 32 (wave + 4 i),
 // in buffer i % 2 of the wave, loaded into register set i % D.
+//
+// Long runs of 2-bit groups are pipelined by one group: iteration i runs the QK
+// phase of group i + 1 (buffer (i + 1) % 2), then the softmax / PV phase of group
+// i (buffer i % 2), so the QK matrix products of one group overlap the softmax and
+// PV chain of the other; then group i + 2 goes into buffer i % 2.  The loads of
+// groups 0 .. D go out together.  Short runs take one group at a time and load
+// group 0 alone first: when every wave of the launch has only a few groups, the
+// first group's latency decides the finish, and the wider first burst of loads
+// delays it (measured on MI355X).
 template <int HD, int KB, int VB>
 __device__ __forceinline__ void kivi_wave_groups(const SegDev& s, const SegOffsets& o,
                                                  const KivLoad& kl, int t_first, int t_end,
@@ -1121,6 +1163,56 @@ __device__ __forceinline__ void kivi_wave_groups(const SegDev& s, const SegOffse
   auto tok = [&](int i) { return t_first + kTile * (wave + kWaves * i); };
   auto buf = [&](int i) { return (i & 1) ? b1 : b0; };
   auto load = [&](R& r, int i) { load_group<HD, KB, VB>(r, s, o, kl, tok(i), t_last, lane); };
+  if constexpr (D == 2) {
+    if (n >= kPipeMinGroups) {
+      auto qk = [&](int i) { return kivi_qk<HD, KB, L>(buf(i), 0, true, qb, sl2, lane); };
+      // set g % D holds group g >= 1 from its load until its store
+      R r0, r[D];
+      load(r0, 0);
+#pragma unroll
+      for (int k = 1; k <= D; ++k) load(r[k % D], k);
+      store_group<HD, KB, VB>(r0, lane, b0);
+      wave_lds_sync();
+      QkOut cur = qk(0);
+      store_group<HD, KB, VB>(r[1], lane, b1);
+      load(r[1], 1 + D);
+      wave_lds_sync();
+      // groups i and i + 1 are in their buffers and cur holds QK(i); groups
+      // i .. i + D + 1 of the steady loop are full
+      int i = 0;
+      for (; i + 2 * D + 1 < n; i += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          const QkOut nxt = qk(i + j + 1);
+          kivi_softmax_pv<HD, KB, VB, true, L>(cur, kTile, buf(i + j), 0, acc, sl2, lane);
+          store_group<HD, KB, VB>(r[(j + 2) % D], lane, buf(i + j));
+          load(r[(j + 2) % D], i + j + 2 + D);
+          wave_lds_sync();
+          cur = nxt;
+        }
+      }
+      for (; i < n; ++i) {
+        QkOut nxt = cur;
+        if (i + 1 < n) nxt = qk(i + 1);
+        const int nvalid = min(kTile, t_end - tok(i));
+        if (nvalid == kTile) kivi_softmax_pv<HD, KB, VB, true, L>(cur, nvalid, buf(i), 0, acc, sl2, lane);
+        else kivi_softmax_pv<HD, KB, VB, false, L>(cur, nvalid, buf(i), 0, acc, sl2, lane);
+        if (i + 2 < n) {
+          const int set = (i + 2) % D;
+#pragma unroll
+          for (int k = 0; k < D; ++k) {
+            if (set == k) {
+              store_group<HD, KB, VB>(r[k], lane, buf(i));
+              if (i + 2 + D < n) load(r[k], i + 2 + D);
+            }
+          }
+          wave_lds_sync();
+        }
+        cur = nxt;
+      }
+      return;
+    }
+  }
   auto group = [&](int i) {
     const int nvalid = min(kTile, t_end - tok(i));
     if (nvalid == kTile) kivi_group<HD, KB, VB, true, L>(nvalid, buf(i), 0, true, qb, acc, sl2, lane);

@@ -115,3 +115,29 @@ def test_mfma_fp16_dense_long(gpu):
     out = dense_fp16_decode(q.to(gpu), k.to(gpu), v.to(gpu), hq).float().cpu().numpy()
     want = ao.segments_attention(q.numpy(), [(k.numpy(), v.numpy())], hq)
     np.testing.assert_allclose(out, want, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("length", [896, 1024, 1056, 1100, 1184, 1311, 1408])
+def test_mfma_long_wave_runs(gpu, hd, length):
+    """One chunk per head group of a 2/2-bit segment: every wave runs 7 to 11 groups, so
+    the waves take the pipelined group loop (8 or more groups) or the one-group-at-a-time
+    loop, with full and ragged last groups on either side of the steady-loop bounds."""
+    from phasekv_amd import decode as dec
+    from phasekv_amd.kernels.packing import quantize_pack
+    print(f"case hd={hd} length={length}", flush=True)
+    g = torch.Generator().manual_seed(length + hd)
+    hq, hkv = 8, 2
+    q = torch.randn(1, hq, hd, generator=g).to(torch.float16)
+    kd = (torch.randn(1, hkv, length, hd, generator=g) * 2).to(torch.float16)
+    vd = torch.randn(1, hkv, length, hd, generator=g).to(torch.float16)
+    pk = quantize_pack(kd.to(gpu), 2, -2, 32)
+    pv = quantize_pack(vd.to(gpu), 2, -1, 32)
+    seg = dec.packed_segment(pk, pv, batched=True, splits=1)
+    fast = _run(q.to(gpu), [seg], hq, False)[0].float().cpu().numpy()
+    slow = _run(q.to(gpu), [seg], hq, True)[0].float().cpu().numpy()
+    deq_k = po.dequantize_float(_np_pt(pk))[0]
+    deq_v = po.dequantize_float(_np_pt(pv))[0]
+    want = ao.segments_attention(q[0].numpy(), [(deq_k, deq_v)], hq)
+    np.testing.assert_allclose(fast, want, atol=2e-3, rtol=1e-2)
+    np.testing.assert_allclose(fast, slow, atol=1e-3, rtol=1e-2)
