@@ -185,6 +185,38 @@ int pk_merge_partials(const float* m, const float* l, const float* acc, int64_t 
                       int32_t n, int32_t head_dim, uint16_t* out, float* out_m,
                       float* out_l, float* out_acc, void* stream);
 
+/* ---- FP16 hot window lifecycle (src/phasekv/phasekv_cache.py) -------------- */
+
+/* Largest number of hot tokens one cooling step can take. */
+#define PK_COOL_MAX_AGED 4096
+
+/* Write one generated token's K and V (fp16 [batch, num_kv_heads, 1, head_dim],
+ * element strides of batch and head given, head_dim contiguous) into row
+ * `position` of the hot window (fp16 [batch, num_kv_heads, capacity, head_dim],
+ * same strides for K and V, head_dim contiguous).  Fails if position is outside
+ * [0, capacity).  Replaces PhaseKVCache.append_hot / _append_token
+ * (src/phasekv/phasekv_cache.py:292-301, 405-422). */
+int pk_append_hot(const uint16_t* k_src, const uint16_t* v_src, int64_t k_bstride,
+                  int64_t k_hstride, int64_t v_bstride, int64_t v_hstride, uint16_t* hot_k,
+                  uint16_t* hot_v, int64_t hot_bstride, int64_t hot_hstride,
+                  int64_t hot_tstride, int batch, int num_kv_heads, int head_dim,
+                  int64_t position, int64_t capacity, void* stream);
+
+/* One lazy cooling step of every (batch, kv head) row of the hot window, in one
+ * launch: rank the oldest `aged` tokens by the float32 L2 norm of their V rows,
+ * keep the `keep` highest (equal norms: the earlier token; NaN above every
+ * number), write the kept K and V rows in token order to out_k / out_v (fp16
+ * [batch, num_kv_heads, keep, head_dim] contiguous) and their token indices to
+ * out_index (int64 [batch, num_kv_heads, keep], may be NULL), then move rows
+ * [aged, hot_len) to [0, hot_len - aged).  keep == aged keeps every token
+ * without ranking.  The caller packs out_k / out_v with pk_quantize_pack into
+ * the new cold segment.  Replaces PhaseKVCache._cool_aged_tokens and _gather_kv
+ * (src/phasekv/phasekv_cache.py:322-340, 110-114). */
+int pk_cool_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride, int64_t hot_hstride,
+                int64_t hot_tstride, int batch, int num_kv_heads, int head_dim,
+                int64_t hot_len, int64_t aged, int64_t keep, uint16_t* out_k,
+                uint16_t* out_v, int64_t* out_index, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

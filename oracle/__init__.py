@@ -7,6 +7,8 @@ HIP kernels in ``phasekv_amd`` implement:
 * ``attention_oracle``     — ``src/phasekv/kernels/reference.py:27-109`` and the
   split/merge math of ``src/phasekv/kernels/attention_triton.py:257-307,604-669``
 * ``launch_config_oracle`` — ``src/phasekv/kernels/launch_config.py:6-64``
+* ``cache_oracle``         — the hot window lifecycle of
+  ``src/phasekv/phasekv_cache.py:101-114,322-340,405-422``
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker.  The product
@@ -25,6 +27,12 @@ Pinning status (what checks each function independently of its own formula):
   reduce/merge) — float64 brute force on tiny inputs, closed forms (uniform
   softmax, one dominant key), and invariants (segment order, split count, LSE
   merge associativity, GQA head mapping).
+* cache_oracle (append, value norms, kept-token selection, cooling) — the
+  selection equals torch's own ``vector_norm(...).topk(k).indices.sort()`` (the
+  calls the reference makes) on tie-free inputs; norms within 1 ulp-scale of a
+  float64 norm; ties and NaN by brute force over explicit rankings; the cooled
+  segment equals ``quantize_pack`` of the kept rows and the shifted window equals
+  slicing; ``keep_count`` against Python's round on half-way cases.
 * plan_kivi_decode — known-answer tests from the reference's
   ``tests/test_phasekv_launch_config.py:10-47`` and the published plan table
   (``docs/idea/PhaseKV-技术原理与系统设计.md:495-502``).

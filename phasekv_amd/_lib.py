@@ -99,6 +99,12 @@ _SIGNATURES = {
                                        _c_vp, _c_vp]),
     "pk_merge_partials": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32, _c_vp,
                                          _c_vp, _c_vp, _c_vp, _c_vp]),
+    "pk_append_hot": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,
+                                     _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, _c_i64, _c_i64, _c_vp]),
+    "pk_cool_hot": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
+                                   ctypes.c_int, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_vp,
+                                   _c_vp, _c_vp, _c_vp]),
 }
 
 _lib = None

@@ -1,0 +1,179 @@
+"""The HIP hot window lifecycle against the oracle: appends, the cooling launch (kept
+indices, gathered rows, shifted tail) bit-exact, and a multi-layer decode loop whose
+cold segments, hot windows and attention output match the oracle's."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_oracle as ao
+from oracle import cache_oracle as co
+from oracle import packing_oracle as po
+
+pytestmark = pytest.mark.gpu
+
+
+def _np_pt(pt):
+    return po.PackedArrays(pt.packed.cpu().numpy(), pt.scale.cpu().numpy(), pt.mins.cpu().numpy(),
+                           pt.bits, pt.axis, pt.group_size, tuple(pt.orig_shape), pt.axis_len)
+
+
+def _u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy()
+
+
+@pytest.mark.parametrize("B,H,hd,cap,hot_len,aged,keep", [
+    (1, 4, 128, 48, 48, 16, 8), (2, 3, 64, 48, 48, 16, 16), (1, 2, 256, 80, 70, 30, 1),
+    (3, 2, 96, 40, 33, 17, 9), (1, 1, 128, 700, 640, 300, 150), (2, 2, 128, 48, 16, 16, 5),
+])
+def test_cool_hot_matches_the_oracle(gpu, B, H, hd, cap, hot_len, aged, keep):
+    from phasekv_amd.cache import cool_hot
+    print(f"case B={B} H={H} hd={hd} hot_len={hot_len} aged={aged} keep={keep}", flush=True)
+    rng = np.random.default_rng(hd + aged + keep)
+    k = (rng.standard_normal((B, H, cap, hd)) * 2).astype(np.float16)
+    v = rng.standard_normal((B, H, cap, hd)).astype(np.float16)
+    if B * H > 1:
+        v[0, 0, 1] = v[0, 0, 0]          # an exact tie of norms (the earlier token wins)
+    hk, hv = torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu)
+    kept_k, kept_v, idx = cool_hot(hk, hv, hot_len, aged, keep, with_index=True)
+    if keep < aged:
+        want_idx = co.select_kept(co.value_norms(v[:, :, :aged]), keep)
+    else:
+        want_idx = np.broadcast_to(np.arange(aged), (B, H, aged))
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    want_k = np.take_along_axis(k[:, :, :aged], want_idx[..., None], axis=2)
+    want_v = np.take_along_axis(v[:, :, :aged], want_idx[..., None], axis=2)
+    assert np.array_equal(_u16(kept_k), want_k.view(np.int16))
+    assert np.array_equal(_u16(kept_v), want_v.view(np.int16))
+    rem = hot_len - aged
+    assert np.array_equal(_u16(hk[:, :, :rem]), k[:, :, aged:hot_len].view(np.int16))
+    assert np.array_equal(_u16(hv[:, :, :rem]), v[:, :, aged:hot_len].view(np.int16))
+    # rows past the old hot length are untouched
+    assert np.array_equal(_u16(hk[:, :, hot_len:]), k[:, :, hot_len:].view(np.int16))
+
+
+def test_cool_hot_nan_rows_rank_first(gpu):
+    from phasekv_amd.cache import cool_hot
+    v = np.ones((1, 1, 20, 64), np.float16)
+    v[0, 0, 9, 3] = np.nan
+    v[0, 0, 4] = 2
+    k = np.zeros_like(v)
+    hk, hv = torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu)
+    _, _, idx = cool_hot(hk, hv, 20, 16, 3, with_index=True)
+    assert idx.cpu().numpy().tolist() == [[[0, 4, 9]]]
+    assert co.select_kept(co.value_norms(v[:, :, :16]), 3).tolist() == [[[0, 4, 9]]]
+
+
+def test_append_hot_writes_one_row(gpu):
+    from phasekv_amd import _lib
+    rng = np.random.default_rng(3)
+    hot = torch.zeros(2, 3, 10, 64, dtype=torch.float16, device=gpu)
+    hot_v = torch.zeros_like(hot)
+    src = torch.from_numpy(rng.standard_normal((2, 3, 1, 64)).astype(np.float16)).to(gpu)
+    src_v = src * 2
+    lib = _lib.load()
+    _lib.check(lib.pk_append_hot(src.data_ptr(), src_v.data_ptr(), src.stride(0), src.stride(1),
+                                 src_v.stride(0), src_v.stride(1), hot.data_ptr(),
+                                 hot_v.data_ptr(), hot.stride(0), hot.stride(1), hot.stride(2),
+                                 2, 3, 64, 7, 10, _lib.stream_ptr(hot.device)), "append_hot")
+    want = torch.zeros(2, 3, 10, 64, dtype=torch.float16)
+    want[:, :, 7:8] = src.cpu()
+    assert torch.equal(hot.cpu(), want)
+    want[:, :, 7:8] = src_v.cpu()
+    assert torch.equal(hot_v.cpu(), want)
+    with pytest.raises(ValueError, match="full"):
+        _lib.check(lib.pk_append_hot(src.data_ptr(), src_v.data_ptr(), 0, 0, 0, 0, hot.data_ptr(),
+                                     hot_v.data_ptr(), hot.stride(0), hot.stride(1), hot.stride(2),
+                                     2, 3, 64, 10, 10, _lib.stream_ptr(hot.device)), "append_hot")
+
+
+class _Dense:
+    def __init__(self, keys, values):
+        self.key_cache, self.value_cache = keys, values
+
+
+@pytest.mark.parametrize("ratio,cold_bits", [(1.0, 4), (0.5, 2), (0.3, 8)])
+def test_decode_loop_matches_the_oracle(gpu, ratio, cold_bits):
+    """Two layers, a selected prompt, 70 decode steps (cooling at steps 48 and 64): cold
+    segments and hot windows bit-exact, and the packed decode over the cache within the
+    attention tolerance of the oracle over the oracle's cache."""
+    from phasekv_amd.cache import PhaseKVCache
+    from phasekv_amd.kernels.attention_triton import fused_phasekv_decode
+    print(f"case ratio={ratio} cold_bits={cold_bits}", flush=True)
+    g = torch.Generator().manual_seed(int(ratio * 10) + cold_bits)
+    L, B, H, hq, hd, S = 2, 1, 2, 8, 128, 200
+    keys = [torch.randn(B, H, S, hd, generator=g).to(torch.float16) for _ in range(L)]
+    values = [torch.randn(B, H, S, hd, generator=g).to(torch.float16) for _ in range(L)]
+    keep = [torch.stack([torch.randperm(S, generator=g)[:150] for _ in range(H)])[None]
+            for _ in range(L)]
+    cache = PhaseKVCache.from_dense_prefill(
+        _Dense([k.to(gpu) for k in keys], [v.to(gpu) for v in values]), prompt_len=S,
+        keep_indices=[i.to(gpu) for i in keep], prompt_bits=2, cold_bits=cold_bits,
+        group_size=32, recent_window=32, lazy_g=16, decode_keep_ratio=ratio)
+    # the oracle's cache
+    ref = []
+    for l in range(L):
+        idx = np.sort(keep[l].numpy(), -1)
+        pk = np.take_along_axis(keys[l].numpy(), idx[..., None], axis=2)
+        pv = np.take_along_axis(values[l].numpy(), idx[..., None], axis=2)
+        ref.append({"prompt": (po.quantize_pack(pk, 2, -2, 32), po.quantize_pack(pv, 2, -1, 32)),
+                    "cold": [], "hot_k": np.zeros((B, H, 48, hd), np.float16),
+                    "hot_v": np.zeros((B, H, 48, hd), np.float16), "hot_len": 0})
+    for l in range(L):
+        got = cache.layer_tiers(l).prompt
+        assert np.array_equal(got.key.packed.cpu().numpy(), ref[l]["prompt"][0].packed)
+        assert np.array_equal(got.value.packed.cpu().numpy(), ref[l]["prompt"][1].packed)
+    q = torch.randn(hq, hd, generator=g).to(torch.float16)
+    for step in range(70):
+        for l in range(L):
+            nk = torch.randn(B, H, 1, hd, generator=g).to(torch.float16)
+            nv = (torch.randn(B, H, 1, hd, generator=g) * (1 + step % 5)).to(torch.float16)
+            cache.append_hot(l, nk.to(gpu), nv.to(gpu))
+            r = ref[l]
+            r["hot_len"] = co.append_hot(r["hot_k"], r["hot_v"], r["hot_len"], nk.numpy(),
+                                         nv.numpy())
+        cache.finish_decode_step()
+        for l in range(L):
+            r = ref[l]
+            seg, r["hot_len"], _ = co.cool_aged_tokens(r["hot_k"], r["hot_v"], r["hot_len"], 32,
+                                                      16, ratio, cold_bits, 32)
+            if seg is not None:
+                r["cold"].append(seg)
+    assert cache.true_seq_length == S + 70
+    for l in range(L):
+        tiers, r = cache.layer_tiers(l), ref[l]
+        assert tiers.hot_len == r["hot_len"] == 38 and len(tiers.cold) == len(r["cold"]) == 2
+        hot_k, hot_v = tiers.hot_views()
+        assert np.array_equal(_u16(hot_k), r["hot_k"][:, :, :r["hot_len"]].view(np.int16))
+        assert np.array_equal(_u16(hot_v), r["hot_v"][:, :, :r["hot_len"]].view(np.int16))
+        for got, (wk, wv) in zip(tiers.cold, r["cold"]):
+            for pt, want in ((got.key, wk), (got.value, wv)):
+                assert pt.group_size == want.group_size
+                assert np.array_equal(pt.packed.cpu().numpy(), want.packed)
+                assert np.array_equal(_u16(pt.scale), want.scale.view(np.int16))
+                assert np.array_equal(_u16(pt.mins), want.mins.view(np.int16))
+        out = fused_phasekv_decode(q.to(gpu), tiers, hq).float().cpu().numpy()
+        segs = [(po.dequantize_float(r["prompt"][0])[0], po.dequantize_float(r["prompt"][1])[0])]
+        segs += [(po.dequantize_float(a)[0], po.dequantize_float(b)[0]) for a, b in r["cold"]]
+        segs.append((r["hot_k"][0, :, :r["hot_len"]], r["hot_v"][0, :, :r["hot_len"]]))
+        want = ao.segments_attention(q.numpy(), segs, hq)
+        np.testing.assert_allclose(out, want, atol=2e-3, rtol=1e-2)
+
+
+def test_decode_step_errors(gpu):
+    from phasekv_amd.cache import PhaseKVCache
+    k = torch.randn(1, 2, 64, 64).to(torch.float16).to(gpu)
+    cache = PhaseKVCache.from_dense_prefill(_Dense([k, k], [k, k]), prompt_len=64,
+                                            recent_window=2, lazy_g=1)
+    tok = torch.zeros(1, 2, 1, 64, dtype=torch.float16, device=gpu)
+    cache.append_hot(0, tok, tok)
+    with pytest.raises(RuntimeError, match="already appended"):
+        cache.append_hot(0, tok, tok)
+    with pytest.raises(RuntimeError, match="missing layers"):
+        cache.finish_decode_step()
+    with pytest.raises(ValueError, match="one token"):
+        cache.append_hot(1, tok[:, :, :0], tok)
+    with pytest.raises(RuntimeError, match="Cache.update"):
+        cache.update(tok, tok, 0)
+    cache.append_hot(1, tok, tok)
+    cache.finish_decode_step()
+    assert cache.get_seq_length() == 65 and cache.true_seq_length == 65
