@@ -19,8 +19,9 @@ counters read for it, from the committed PMC summary.
 
 Prints ONE JSON line (rank 0).  Extra fields: ``us_per_step``, the FP16 dense
 GQA-aware comparator on the same tokens, and ``sweep``: the same measurement
-for the context sweep (C3), the batched configurations (C4, C5) and C4's
-prefill-side quantize + pack of an 8192 x 4 x 128 K/V block.
+for the context sweep (C3), the batched configurations (C4, C5), C4's
+prefill-side quantize + pack of an 8192 x 4 x 128 K/V block, and the hot window
+lifecycle (append per step, one cooling event) at the C2 and C5 cache shapes.
 """
 from __future__ import annotations
 
@@ -147,6 +148,66 @@ def _bench_prefill_pack(device, steps, warmup, stream):
             "frac": nbytes / sec / 1e9 / HBM_PEAK_GBS}
 
 
+def _bench_lifecycle(cfg, device, steps, warmup, stream, ratio, with_cpu):
+    """The hot window lifecycle of one layer at ``cfg``'s cache shape (recent window 32,
+    lazy_g 16, 4-bit cold segments: ``phasekv_cache.py:185-196`` defaults): the
+    ``append_hot`` launch of every decode step, and one cooling event (one launch
+    that ranks, gathers and packs the new segment and shifts the window; the
+    three-launch form, cooling then two ``quantize_pack``, is timed beside it),
+    which fires once every lazy_g steps.  Both are latency-bound: a cooling event moves
+    ``B * Hkv * 48`` rows of ``hd`` fp16 values.
+    """
+    from phasekv_amd import _lib
+    from phasekv_amd.cache import cool_hot, cool_pack_hot, cool_pack_supported, keep_count
+    from phasekv_amd.kernels.packing import quantize_pack
+    window, lazy_g, bits = 32, 16, 4
+    cap = window + lazy_g
+    B, H, D = cfg.batch, cfg.hkv, cfg.hd
+    gen = torch.Generator().manual_seed(1234)
+    hot_k = torch.randn(B, H, cap, D, generator=gen).to(torch.float16).to(device)
+    hot_v = torch.randn(B, H, cap, D, generator=gen).to(torch.float16).to(device)
+    tok = torch.randn(B, H, 1, D, generator=gen).to(torch.float16).to(device)
+    keep = keep_count(lazy_g, ratio)
+    lib = _lib.load()
+
+    def append():
+        _lib.check(lib.pk_append_hot(tok.data_ptr(), tok.data_ptr(), tok.stride(0), tok.stride(1),
+                                     tok.stride(0), tok.stride(1), hot_k.data_ptr(),
+                                     hot_v.data_ptr(), hot_k.stride(0), hot_k.stride(1),
+                                     hot_k.stride(2), B, H, D, cap - 1, cap,
+                                     _lib.stream_ptr(device)), "append_hot")
+
+    def cool():
+        cool_pack_hot(hot_k, hot_v, cap, lazy_g, keep, bits, 32)
+
+    def cool_unfused():
+        k, v, _ = cool_hot(hot_k, hot_v, cap, lazy_g, keep)
+        quantize_pack(k, bits, -2, 32)
+        quantize_pack(v, bits, -1, 32)
+
+    a_sec = _time_graph([append], steps, warmup, stream)
+    c_sec = _time_graph([cool], steps, warmup, stream)
+    u_sec = _time_graph([cool_unfused], steps, warmup, stream)
+    res = {"config": f"{cfg.name}-lifecycle", "shape": [B, H, cap, D], "recent_window": window,
+           "lazy_g": lazy_g, "decode_keep_ratio": ratio, "cold_bits": bits,
+           "append_us": a_sec * 1e6, "cooling_us": c_sec * 1e6,
+           "cooling_three_launches_us": u_sec * 1e6, "fused": cool_pack_supported(
+               hot_k, hot_v, cap, lazy_g, keep, 32),
+           "us_per_layer_step": (a_sec + c_sec / lazy_g) * 1e6}
+    if with_cpu:
+        # the numpy oracle of the same event on the host: the reference's CPU path
+        from oracle import cache_oracle as co
+        hk, hv = hot_k.cpu().numpy(), hot_v.cpu().numpy()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 1.0:
+            co.cool_aged_tokens(hk.copy(), hv.copy(), cap, window, lazy_g, ratio, bits, 32)
+            n += 1
+        res["cpu_cooling_us"] = (time.perf_counter() - t0) / n * 1e6
+    del hot_k, hot_v
+    torch.cuda.empty_cache()
+    return res
+
+
 def _cpu_baseline(cfg_name: str, budget_s: float = 10.0):
     """The oracle (reference.py semantics in numpy) on host cores, bounded sample."""
     import numpy as np
@@ -256,6 +317,11 @@ def main() -> int:
         r = _bench_prefill_pack(device, min(args.steps, 128), min(args.warmup, 128), stream)
         _log(f"bench: C4-prefill-pack {r}")
         sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+        for name, ratio in (("C2", 1.0), ("C2", 0.5), ("C5", 0.5)):
+            r = _bench_lifecycle(workloads.CONFIGS[name], device, min(args.steps, 128),
+                                 min(args.warmup, 128), stream, ratio, not args.no_cpu)
+            _log(f"bench: lifecycle {r}")
+            sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
     cpu = None
     if not args.no_cpu:
         cpu = _cpu_baseline(cfg.name if cfg.batch == 1 else "C2", args.cpu_seconds)

@@ -217,6 +217,28 @@ int pk_cool_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride, int64_t h
                 int64_t hot_len, int64_t aged, int64_t keep, uint16_t* out_k,
                 uint16_t* out_v, int64_t* out_index, void* stream);
 
+/* 1 if pk_cool_pack_hot takes this window (the row's hot window and the
+ * packing statistics fit one workgroup's LDS and head_dim % 8 == 0), else 0. */
+int pk_cool_pack_supported(int64_t hot_len, int head_dim, int64_t aged, int64_t keep,
+                           int group_size);
+
+/* pk_cool_hot and the packing of the new cold segment in one launch: the kept
+ * rows are quantized with `bits` and `group_size` exactly as pk_quantize_pack
+ * would (K along the kept tokens, group min(group_size, keep); V along head_dim,
+ * group min(group_size, head_dim)) and written in the storage pk_quantize_pack
+ * gives them: K codes [batch, num_kv_heads, ceil(keep / vpb), head_dim] and
+ * K scale / mins [batch, num_kv_heads, n_groups, head_dim] (its transposed
+ * layout), V codes [batch, num_kv_heads, keep, ceil(head_dim / vpb)] and V scale
+ * / mins [batch, num_kv_heads, keep, n_groups], all contiguous.  Hot buffers in
+ * 16-byte pieces (16-byte aligned, strides multiples of 8).  Fails without a
+ * launch when pk_cool_pack_supported is 0.  Replaces _cool_aged_tokens with its
+ * _pack_kv (src/phasekv/phasekv_cache.py:322-340, 101-107). */
+int pk_cool_pack_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride, int64_t hot_hstride,
+                     int64_t hot_tstride, int batch, int num_kv_heads, int head_dim,
+                     int64_t hot_len, int64_t aged, int64_t keep, int bits, int group_size,
+                     uint8_t* k_packed, uint16_t* k_scale, uint16_t* k_mins, uint8_t* v_packed,
+                     uint16_t* v_scale, uint16_t* v_mins, int64_t* out_index, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

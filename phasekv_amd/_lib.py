@@ -105,6 +105,12 @@ _SIGNATURES = {
     "pk_cool_hot": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
                                    ctypes.c_int, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_vp,
                                    _c_vp, _c_vp, _c_vp]),
+    "pk_cool_pack_supported": (ctypes.c_int, [_c_i64, ctypes.c_int, _c_i64, _c_i64,
+                                              ctypes.c_int]),
+    "pk_cool_pack_hot": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, _c_i64, _c_i64, _c_i64,
+                                        ctypes.c_int, ctypes.c_int, _c_vp, _c_vp, _c_vp, _c_vp,
+                                        _c_vp, _c_vp, _c_vp, _c_vp]),
 }
 
 _lib = None

@@ -11,8 +11,9 @@ decode loop:
   ``:405-422`` (one HIP launch writes K and V)
 * ``finish_decode_step``   ``phasekv_cache.py:302-320``
 * ``_cool_aged_tokens``    ``phasekv_cache.py:322-340``: one HIP launch ranks the
-  aged tokens by value norm, gathers the kept ones and shifts the hot tail, then
-  two ``quantize_pack`` launches pack the new cold segment
+  aged tokens by value norm, gathers and packs the kept ones into the new cold
+  segment and shifts the hot tail (windows too large for one workgroup's LDS:
+  a cooling launch, then two ``quantize_pack`` launches)
 * accessors ``__len__``, ``layer_tiers``, ``get_seq_length``, ``get_max_cache_shape``,
   ``true_seq_length``, ``physical_nbytes`` (``:265-289``, ``:436-445``)
 
@@ -30,7 +31,7 @@ from typing import Optional, Sequence
 import torch
 
 from . import _lib
-from .kernels.packing import quantize_pack
+from .kernels.packing import PackedTensor, quantize_pack
 from .tiers import LayerTiers, PackedKVSegment, pack_kv
 
 _PACKED_BITS = (2, 4, 8)
@@ -95,6 +96,64 @@ def cool_hot(hot_k: torch.Tensor, hot_v: torch.Tensor, hot_len: int, aged: int, 
                                index.data_ptr() if index is not None else None,
                                _lib.stream_ptr(dev)), "cool_hot")
     return kept_k, kept_v, index
+
+
+def cool_pack_hot(hot_k: torch.Tensor, hot_v: torch.Tensor, hot_len: int, aged: int, keep: int,
+                  bits: int, group_size: int, with_index: bool = False):
+    """One cooling step and the packing of its cold segment in one launch.
+
+    Returns ``(segment, index)``: a ``PackedKVSegment`` identical to
+    ``pack_kv(kept_k, kept_v, bits, group_size)`` over the rows ``cool_hot`` would
+    keep (the same tensors, shapes and views ``quantize_pack`` gives), and the kept
+    token indices if asked.  Windows the fused launch does not take (see
+    ``cool_pack_supported``) go through ``cool_hot`` and two ``quantize_pack``
+    launches instead.
+    """
+    dev = _lib.require_device(hot_k, hot_v)
+    B, H, _, D = hot_k.shape
+    if not cool_pack_supported(hot_k, hot_v, hot_len, aged, keep, group_size):
+        key, value, index = cool_hot(hot_k, hot_v, hot_len, aged, keep, with_index)
+        return PackedKVSegment(quantize_pack(key, bits, axis=-2, group_size=group_size),
+                               quantize_pack(value, bits, axis=-1, group_size=group_size)), index
+    if bits not in _PACKED_BITS:
+        raise ValueError(f"bits must be one of {_PACKED_BITS}, got {bits}")
+    vpb = 8 // bits
+    gsk, gsv = min(group_size, keep), min(group_size, D)
+    ngk, nbk = -(-keep // gsk), -(-keep // vpb)
+    ngv, nbv = -(-D // gsv), -(-D // vpb)
+    u8, f16 = torch.uint8, torch.float16
+    # the storage quantize_pack gives K (axis -2: transposed views) and V (axis -1)
+    kp = torch.empty(B, H, nbk, D, dtype=u8, device=dev).transpose(-1, -2)
+    ks = torch.empty(B, H, ngk, D, dtype=f16, device=dev).transpose(-1, -2)
+    km = torch.empty(B, H, ngk, D, dtype=f16, device=dev).transpose(-1, -2)
+    vp = torch.empty(B, H, keep, nbv, dtype=u8, device=dev)
+    vs = torch.empty(B, H, keep, ngv, dtype=f16, device=dev)
+    vm = torch.empty(B, H, keep, ngv, dtype=f16, device=dev)
+    index = torch.empty(B, H, keep, dtype=torch.int64, device=dev) if with_index else None
+    lib = _lib.load()
+    _lib.check(lib.pk_cool_pack_hot(hot_k.data_ptr(), hot_v.data_ptr(), hot_k.stride(0),
+                                    hot_k.stride(1), hot_k.stride(2), B, H, D, hot_len, aged,
+                                    keep, bits, group_size, kp.data_ptr(), ks.data_ptr(),
+                                    km.data_ptr(), vp.data_ptr(), vs.data_ptr(), vm.data_ptr(),
+                                    index.data_ptr() if index is not None else None,
+                                    _lib.stream_ptr(dev)), "cool_pack_hot")
+    shape = (B, H, keep, D)
+    key = PackedTensor(packed=kp, scale=ks, mins=km, bits=bits, axis=2, group_size=gsk,
+                       orig_shape=shape, axis_len=keep)
+    value = PackedTensor(packed=vp, scale=vs, mins=vm, bits=bits, axis=3, group_size=gsv,
+                         orig_shape=shape, axis_len=D)
+    return PackedKVSegment(key, value), index
+
+
+def cool_pack_supported(hot_k: torch.Tensor, hot_v: torch.Tensor, hot_len: int, aged: int,
+                        keep: int, group_size: int) -> bool:
+    """Whether ``cool_pack_hot`` runs as one launch for these buffers and sizes."""
+    D = hot_k.shape[-1]
+    pieces = all(s % 8 == 0 for s in hot_k.stride()[:3]) and hot_k.stride() == hot_v.stride()
+    aligned = hot_k.data_ptr() % 16 == 0 and hot_v.data_ptr() % 16 == 0
+    return bool(pieces and aligned and hot_k.stride(-1) == 1 and hot_k.dtype == torch.float16
+                and hot_v.dtype == torch.float16
+                and _lib.load().pk_cool_pack_supported(hot_len, D, aged, keep, group_size))
 
 
 class PhaseKVCache:
@@ -302,8 +361,7 @@ class PhaseKVCache:
         if aged < self.lazy_g:
             return
         keep = keep_count(aged, self.decode_keep_ratio)
-        key, value, _ = cool_hot(layer.hot_k, layer.hot_v, layer.hot_len, aged, keep)
-        layer.cold.append(PackedKVSegment(
-            quantize_pack(key, self.cold_bits, axis=-2, group_size=self.group_size),
-            quantize_pack(value, self.cold_bits, axis=-1, group_size=self.group_size)))
+        segment, _ = cool_pack_hot(layer.hot_k, layer.hot_v, layer.hot_len, aged, keep,
+                                   self.cold_bits, self.group_size)
+        layer.cold.append(segment)
         layer.hot_len -= aged

@@ -9,6 +9,7 @@
 // The cooled tokens are packed afterwards by pk_quantize_pack (the cache's
 // _pack_kv, phasekv_cache.py:101-107).
 #include "pk_common.h"
+#include "pk_quant.h"
 
 #include <algorithm>
 
@@ -18,6 +19,7 @@ namespace {
 
 constexpr int kCoolThreads = 256;
 constexpr int kCoolWaves = kCoolThreads / 64;
+constexpr size_t kCoolStagedLds = 64 * 1024;   // dynamic LDS of the staged cooling kernel
 
 struct HotView {
   int64_t bs, hs, ts;   // element strides of batch, kv head, token; head_dim is contiguous
@@ -125,7 +127,233 @@ cool_hot_kernel(uint16_t* hk, uint16_t* hv, HotView hot, int Hkv, int hd, int ho
   }
 }
 
+// The same cooling step with the whole window of the row staged in LDS first:
+// every global read is issued at once (16-byte pieces), the norms, the ranking,
+// the gather and the shift then work from LDS, and the shift has no overlap
+// hazard (its sources are in LDS).  Needs head_dim, the token stride and both
+// bases in whole 16-byte pieces; LDS holds 4 * hot_len * head_dim bytes plus
+// 8 bytes per aged token (plus the packing statistics of the fused variant).
+struct Staged {
+  uint4* sk;      // [hot_len][hd / 8]
+  uint4* sv;
+  int* pos;       // [aged]: output row of a kept token, -1 otherwise
+  char* tail;     // first free byte
+};
+
+__device__ __forceinline__ Staged stage_and_select(const uint16_t* krow0, const uint16_t* vrow0,
+                                                   int64_t ts, int hd, int hot_len, int aged,
+                                                   int keep, char* lds) {
+  const int pr = hd / 8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  Staged st;
+  st.sk = reinterpret_cast<uint4*>(lds);
+  st.sv = st.sk + hot_len * pr;
+  float* norm = reinterpret_cast<float*>(st.sv + hot_len * pr);
+  st.pos = reinterpret_cast<int*>(norm + aged);
+  st.tail = reinterpret_cast<char*>(st.pos + aged);
+  for (int i = tid; i < hot_len * pr; i += kCoolThreads) {
+    const int t = i / pr, c = i - t * pr;
+    st.sk[i] = *reinterpret_cast<const uint4*>(krow0 + t * ts + 8 * c);
+    st.sv[i] = *reinterpret_cast<const uint4*>(vrow0 + t * ts + 8 * c);
+  }
+  __syncthreads();
+  const uint16_t* svh = reinterpret_cast<const uint16_t*>(st.sv);
+  if (keep < aged) {
+    // norms: each wave takes 4 tokens at a time, their butterflies interleaved
+    // (the same per-token order as the one-token loop)
+    for (int t0 = wave; t0 < aged; t0 += 4 * kCoolWaves) {
+      float s[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = min(t0 + j * kCoolWaves, aged - 1);
+        const uint16_t* v = svh + t * hd;
+        s[j] = 0.f;
+        for (int c = lane; c < hd; c += 64) {
+          const float x = pk_h2f(v[c]);
+          s[j] = __fadd_rn(s[j], __fmul_rn(x, x));
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] = __fadd_rn(s[j], __shfl_xor(s[j], o));
+      if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (t0 + j * kCoolWaves < aged) norm[t0 + j * kCoolWaves] = __fsqrt_rn(s[j]);
+      }
+    }
+    __syncthreads();
+    // wave 0 ranks 64 tokens at a time; output rows by ballot prefix counts
+    if (wave == 0) {
+      int count = 0;
+      for (int base = 0; base < aged; base += 64) {
+        const int t = base + lane;
+        bool kept = false;
+        if (t < aged) {
+          const float nt = norm[t];
+          int rank = 0;
+          for (int u = 0; u < aged; ++u) rank += ranks_above(norm[u], u, nt, t) ? 1 : 0;
+          kept = rank < keep;
+        }
+        const uint64_t mask = __ballot(kept);
+        if (t < aged) st.pos[t] = kept ? count + __popcll(mask & ((1ull << lane) - 1ull)) : -1;
+        count += __popcll(mask);
+      }
+    }
+  } else {
+    for (int t = tid; t < aged; t += kCoolThreads) st.pos[t] = t;
+  }
+  __syncthreads();
+  return st;
+}
+
+// rows [aged, hot_len) of the staged window back to rows [0, hot_len - aged)
+__device__ __forceinline__ void shift_from_lds(const Staged& st, uint16_t* krow0, uint16_t* vrow0,
+                                               int64_t ts, int hd, int hot_len, int aged) {
+  const int pr = hd / 8;
+  const int remaining = hot_len - aged;
+  for (int i = threadIdx.x; i < remaining * pr; i += kCoolThreads) {
+    const int r = i / pr, c = i - r * pr;
+    *reinterpret_cast<uint4*>(krow0 + r * ts + 8 * c) = st.sk[i + aged * pr];
+    *reinterpret_cast<uint4*>(vrow0 + r * ts + 8 * c) = st.sv[i + aged * pr];
+  }
+}
+
+__global__ void __launch_bounds__(kCoolThreads)
+cool_hot_staged_kernel(uint16_t* hk, uint16_t* hv, HotView hot, int Hkv, int hd, int hot_len,
+                       int aged, int keep, uint16_t* __restrict__ ok, uint16_t* __restrict__ ov,
+                       int64_t* __restrict__ oidx) {
+  extern __shared__ __attribute__((aligned(16))) char lds_c[];
+  const int64_t b = blockIdx.x / Hkv, h = blockIdx.x - b * Hkv;
+  uint16_t* krow0 = hk + b * hot.bs + h * hot.hs;
+  uint16_t* vrow0 = hv + b * hot.bs + h * hot.hs;
+  const Staged st = stage_and_select(krow0, vrow0, hot.ts, hd, hot_len, aged, keep, lds_c);
+  const int pr = hd / 8;
+  const int64_t obase = ((int64_t)b * Hkv + h) * keep;
+  uint4* okq = reinterpret_cast<uint4*>(ok);
+  uint4* ovq = reinterpret_cast<uint4*>(ov);
+  for (int i = threadIdx.x; i < aged * pr; i += kCoolThreads) {
+    const int t = i / pr, c = i - t * pr;
+    const int j = st.pos[t];
+    if (j < 0) continue;
+    okq[(obase + j) * pr + c] = st.sk[i];
+    ovq[(obase + j) * pr + c] = st.sv[i];
+    if (oidx && c == 0) oidx[obase + j] = t;
+  }
+  shift_from_lds(st, krow0, vrow0, hot.ts, hd, hot_len, aged);
+}
+
+// Outputs of the fused cooling + packing step, in the storage quantize_pack
+// gives the cache's segments (phasekv_cache.py:101-107): K grouped along the
+// kept tokens, codes [B*Hkv][nbk][hd] and scale / min [B*Hkv][ngk][hd] (token
+// bytes and groups outermost); V grouped along head_dim, codes
+// [B*Hkv*keep][nbv] and scale / min [B*Hkv*keep][ngv].
+struct PackOut {
+  uint8_t* kp;
+  uint16_t* ks;
+  uint16_t* km;
+  uint8_t* vp;
+  uint16_t* vs;
+  uint16_t* vm;
+  int bits, gsk, ngk, nbk, gsv, ngv, nbv;
+};
+
+__global__ void __launch_bounds__(kCoolThreads)
+cool_pack_staged_kernel(uint16_t* hk, uint16_t* hv, HotView hot, int Hkv, int hd, int hot_len,
+                        int aged, int keep, PackOut po, int64_t* __restrict__ oidx) {
+  extern __shared__ __attribute__((aligned(16))) char lds_c[];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x / Hkv, h = blockIdx.x - b * Hkv;
+  const int64_t bh = (int64_t)b * Hkv + h;
+  uint16_t* krow0 = hk + b * hot.bs + h * hot.hs;
+  uint16_t* vrow0 = hv + b * hot.bs + h * hot.hs;
+  const Staged st = stage_and_select(krow0, vrow0, hot.ts, hd, hot_len, aged, keep, lds_c);
+  int* kidx = reinterpret_cast<int*>(st.tail);                      // [keep]: token of kept row
+  pk::GroupStats* kst = reinterpret_cast<pk::GroupStats*>(kidx + keep + (keep & 1));  // [ngk][hd]
+  pk::GroupStats* vst = kst + po.ngk * hd;                            // [keep][ngv]
+  for (int t = tid; t < aged; t += kCoolThreads)
+    if (st.pos[t] >= 0) kidx[st.pos[t]] = t;
+  __syncthreads();
+  const uint16_t* skh = reinterpret_cast<const uint16_t*>(st.sk);
+  const uint16_t* svh = reinterpret_cast<const uint16_t*>(st.sv);
+  // group statistics and the fp16 scale / min
+  for (int i = tid; i < po.ngk * hd; i += kCoolThreads) {
+    const int g = i / hd, c = i - g * hd;
+    const int j0 = g * po.gsk, j1 = min(j0 + po.gsk, keep);
+    float mn = pk_h2f(skh[kidx[j0] * hd + c]), mx = mn;
+    for (int j = j0 + 1; j < j1; ++j) {
+      const float x = pk_h2f(skh[kidx[j] * hd + c]);
+      mn = pk::nan_min(mn, x);
+      mx = pk::nan_max(mx, x);
+    }
+    const pk::GroupStats s = pk::group_stats_from(mn, mx, po.bits);
+    kst[i] = s;
+    po.ks[(bh * po.ngk + g) * hd + c] = pk_f2h(s.scale);
+    po.km[(bh * po.ngk + g) * hd + c] = pk_f2h(s.mn);
+  }
+  for (int i = tid; i < keep * po.ngv; i += kCoolThreads) {
+    const int j = i / po.ngv, g = i - j * po.ngv;
+    const uint16_t* row = svh + kidx[j] * hd;
+    const int c0 = g * po.gsv, c1 = min(c0 + po.gsv, hd);
+    float mn = pk_h2f(row[c0]), mx = mn;
+    for (int c = c0 + 1; c < c1; ++c) {
+      const float x = pk_h2f(row[c]);
+      mn = pk::nan_min(mn, x);
+      mx = pk::nan_max(mx, x);
+    }
+    const pk::GroupStats s = pk::group_stats_from(mn, mx, po.bits);
+    vst[i] = s;
+    po.vs[(bh * keep + j) * po.ngv + g] = pk_f2h(s.scale);
+    po.vm[(bh * keep + j) * po.ngv + g] = pk_f2h(s.mn);
+  }
+  __syncthreads();
+  // code bytes, LSB first, zero codes past the end of the axis
+  const int vpb = 8 / po.bits;
+  for (int i = tid; i < po.nbk * hd; i += kCoolThreads) {
+    const int byte = i / hd, c = i - byte * hd;
+    uint32_t x = 0;
+    for (int k = 0; k < vpb; ++k) {
+      const int j = byte * vpb + k;
+      if (j < keep)
+        x |= pk::quant_code(pk_h2f(skh[kidx[j] * hd + c]), kst[(j / po.gsk) * hd + c], po.bits)
+             << (k * po.bits);
+    }
+    po.kp[(bh * po.nbk + byte) * hd + c] = static_cast<uint8_t>(x);
+  }
+  for (int i = tid; i < keep * po.nbv; i += kCoolThreads) {
+    const int j = i / po.nbv, byte = i - j * po.nbv;
+    const uint16_t* row = svh + kidx[j] * hd;
+    uint32_t x = 0;
+    for (int k = 0; k < vpb; ++k) {
+      const int c = byte * vpb + k;
+      if (c < hd)
+        x |= pk::quant_code(pk_h2f(row[c]), vst[j * po.ngv + c / po.gsv], po.bits) << (k * po.bits);
+    }
+    po.vp[(bh * keep + j) * po.nbv + byte] = static_cast<uint8_t>(x);
+  }
+  if (oidx)
+    for (int j = tid; j < keep; j += kCoolThreads) oidx[bh * keep + j] = kidx[j];
+  shift_from_lds(st, krow0, vrow0, hot.ts, hd, hot_len, aged);
+}
+
+// LDS bytes of the staged kernels (0 if the row does not stage)
+static size_t staged_lds(int64_t hot_len, int hd, int64_t aged, int64_t keep, bool pack,
+                         int64_t ngk, int64_t ngv) {
+  if (hd % 8) return 0;
+  size_t bytes = (size_t)4 * hot_len * hd + (size_t)8 * aged;
+  if (pack) bytes += (size_t)4 * (keep + (keep & 1)) + sizeof(pk::GroupStats) * (ngk * hd + keep * ngv);
+  return bytes <= kCoolStagedLds ? bytes : 0;
+}
+
 }  // namespace
+
+// 16-byte pieces of the hot rows
+static bool hot_vectors(const uint16_t* hk, const uint16_t* hv, int hd, int64_t bs, int64_t hs,
+                        int64_t ts) {
+  return hd % 8 == 0 && ts % 8 == 0 && bs % 8 == 0 && hs % 8 == 0 &&
+         reinterpret_cast<uintptr_t>(hk) % 16 == 0 && reinterpret_cast<uintptr_t>(hv) % 16 == 0;
+}
 
 static int check_hot(const uint16_t* hk, const uint16_t* hv, int batch, int hkv, int hd,
                      int64_t hbs, int64_t hhs, int64_t hts) {
@@ -169,10 +397,72 @@ extern "C" int pk_cool_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride
   if (aged > PK_COOL_MAX_AGED) return pk::fail("aged above PK_COOL_MAX_AGED");
   if (keep <= 0 || keep > aged) return pk::fail("keep must be in [1, aged]");
   if (!out_k || !out_v) return pk::fail("null output buffer");
-  const size_t lds = (size_t)aged * (sizeof(float) + 2 * sizeof(int));
+  const size_t meta = (size_t)aged * (sizeof(float) + 2 * sizeof(int));
+  const size_t staged = staged_lds(hot_len, head_dim, aged, keep, false, 0, 0);
+  const bool vec = hot_vectors(hot_k, hot_v, head_dim, hot_bstride, hot_hstride, hot_tstride) &&
+                   reinterpret_cast<uintptr_t>(out_k) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out_v) % 16 == 0;
+  if (vec && staged) {
+    hipLaunchKernelGGL(cool_hot_staged_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads),
+                       staged, static_cast<hipStream_t>(stream), hot_k, hot_v,
+                       HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
+                       (int)hot_len, (int)aged, (int)keep, out_k, out_v, out_index);
+    return pk::check_launch("cool_hot");
+  }
+  const size_t lds = meta;
   hipLaunchKernelGGL(cool_hot_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads), lds,
                      static_cast<hipStream_t>(stream), hot_k, hot_v,
                      HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
                      (int)hot_len, (int)aged, (int)keep, out_k, out_v, out_index);
   return pk::check_launch("cool_hot");
+}
+
+extern "C" int pk_cool_pack_supported(int64_t hot_len, int head_dim, int64_t aged, int64_t keep,
+                                      int group_size) {
+  if (hot_len <= 0 || head_dim <= 0 || aged <= 0 || aged > hot_len || keep <= 0 || keep > aged ||
+      group_size <= 0)
+    return 0;
+  const int64_t ngk = pk::cdiv(keep, std::min<int64_t>(group_size, keep));
+  const int64_t ngv = pk::cdiv(head_dim, std::min<int64_t>(group_size, head_dim));
+  return staged_lds(hot_len, head_dim, aged, keep, true, ngk, ngv) ? 1 : 0;
+}
+
+extern "C" int pk_cool_pack_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride,
+                                int64_t hot_hstride, int64_t hot_tstride, int batch,
+                                int num_kv_heads, int head_dim, int64_t hot_len, int64_t aged,
+                                int64_t keep, int bits, int group_size, uint8_t* k_packed,
+                                uint16_t* k_scale, uint16_t* k_mins, uint8_t* v_packed,
+                                uint16_t* v_scale, uint16_t* v_mins, int64_t* out_index,
+                                void* stream) {
+  pk::clear_error();
+  if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
+                         hot_tstride))
+    return rc;
+  if (aged <= 0 || aged > hot_len) return pk::fail("aged must be in [1, hot_len]");
+  if (keep <= 0 || keep > aged) return pk::fail("keep must be in [1, aged]");
+  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+  if (group_size <= 0) return pk::fail("group_size must be positive");
+  if (!k_packed || !k_scale || !k_mins || !v_packed || !v_scale || !v_mins)
+    return pk::fail("null output buffer");
+  if (!pk_cool_pack_supported(hot_len, head_dim, aged, keep, group_size) ||
+      !hot_vectors(hot_k, hot_v, head_dim, hot_bstride, hot_hstride, hot_tstride))
+    return pk::fail("this window does not fit the fused cooling step "
+                    "(use pk_cool_hot and pk_quantize_pack)");
+  PackOut po;
+  po.kp = k_packed; po.ks = k_scale; po.km = k_mins;
+  po.vp = v_packed; po.vs = v_scale; po.vm = v_mins;
+  po.bits = bits;
+  const int vpb = 8 / bits;
+  po.gsk = (int)std::min<int64_t>(group_size, keep);
+  po.ngk = (int)pk::cdiv(keep, po.gsk);
+  po.nbk = (int)pk::cdiv(keep, vpb);
+  po.gsv = std::min(group_size, head_dim);
+  po.ngv = (int)pk::cdiv(head_dim, po.gsv);
+  po.nbv = (int)pk::cdiv(head_dim, vpb);
+  const size_t lds = staged_lds(hot_len, head_dim, aged, keep, true, po.ngk, po.ngv);
+  hipLaunchKernelGGL(cool_pack_staged_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads),
+                     lds, static_cast<hipStream_t>(stream), hot_k, hot_v,
+                     HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
+                     (int)hot_len, (int)aged, (int)keep, po, out_index);
+  return pk::check_launch("cool_pack_hot");
 }

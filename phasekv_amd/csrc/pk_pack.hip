@@ -9,6 +9,7 @@
 // intrinsics (no contraction, no fast reciprocal) so the outputs are
 // bit-identical to the reference run by torch.
 #include "pk_common.h"
+#include "pk_quant.h"
 
 // No multiply-add contraction anywhere in this file: the reference multiplies
 // and adds in separate float32 operations.
@@ -113,14 +114,10 @@ __device__ __forceinline__ float load_x(const QuantParams& p, int64_t off) {
   return static_cast<const float*>(p.x)[off];
 }
 
-// min / max with NaN propagation (torch.amin / amax semantics).
-__device__ __forceinline__ float nan_min(float a, float b) { return (b < a || b != b) ? b : a; }
-__device__ __forceinline__ float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
-
-struct GroupStats {
-  float mn;
-  float scale;   // float32 scale used for the codes (the fp16 copy is what is stored)
-};
+using pk::GroupStats;
+using pk::nan_max;
+using pk::nan_min;
+using pk::quant_code;
 
 // Statistics of group g of the row at base offset `off`.  The reference pads the
 // tail group with copies of the last element, which changes neither its min nor
@@ -135,17 +132,7 @@ __device__ __forceinline__ GroupStats group_stats(const QuantParams& p, int64_t 
     mn = nan_min(mn, v);
     mx = nan_max(mx, v);
   }
-  float range = __fsub_rn(mx, mn);
-  range = (range < 1e-8f) ? 1e-8f : range;           // clamp_(min=1e-8), NaN kept
-  const float qmax = static_cast<float>((1 << p.bits) - 1);
-  return GroupStats{mn, __fdiv_rn(range, qmax)};
-}
-
-__device__ __forceinline__ uint32_t quant_code(float v, const GroupStats& s, int bits) {
-  const float qmax = static_cast<float>((1 << bits) - 1);
-  float q = rintf(__fdiv_rn(__fsub_rn(v, s.mn), s.scale));   // round half to even
-  q = fminf(fmaxf(q, 0.0f), qmax);
-  return static_cast<uint32_t>(q);
+  return pk::group_stats_from(mn, mx, p.bits);
 }
 
 // One thread per (row, group) when whole groups cover whole bytes (gs % vpb == 0).
@@ -201,9 +188,7 @@ __device__ __forceinline__ GroupStats stats32(const float (&v)[32], int bits) {
     mn = nan_min(mn, v[i]);
     mx = nan_max(mx, v[i]);
   }
-  float range = __fsub_rn(mx, mn);
-  range = (range < 1e-8f) ? 1e-8f : range;
-  return GroupStats{mn, __fdiv_rn(range, static_cast<float>((1 << bits) - 1))};
+  return pk::group_stats_from(mn, mx, bits);
 }
 
 // Groups along the contiguous axis (V, per token along head_dim): one thread

@@ -177,3 +177,47 @@ def test_decode_step_errors(gpu):
     cache.append_hot(1, tok, tok)
     cache.finish_decode_step()
     assert cache.get_seq_length() == 65 and cache.true_seq_length == 65
+
+
+@pytest.mark.parametrize("B,H,hd,cap,hot_len,aged,keep,bits,gs", [
+    (1, 4, 128, 48, 48, 16, 16, 4, 32), (1, 4, 128, 48, 48, 16, 8, 2, 32),
+    (2, 3, 64, 48, 40, 16, 5, 2, 32), (1, 2, 96, 64, 60, 24, 24, 8, 32),
+    (2, 2, 128, 48, 48, 16, 16, 4, 4), (1, 2, 128, 48, 48, 16, 12, 2, 5),
+    (1, 1, 64, 40, 17, 17, 3, 4, 2), (1, 2, 256, 80, 70, 30, 7, 4, 32),
+])
+def test_cool_pack_hot_matches_cool_then_quantize(gpu, B, H, hd, cap, hot_len, aged, keep, bits, gs):
+    """The fused cooling + packing launch against the oracle's selection, gather and
+    quantize_pack, bit for bit, with the same shapes and views as quantize_pack's output;
+    the last case does not fit one workgroup's LDS and takes the three-launch path."""
+    from phasekv_amd.cache import cool_pack_hot, cool_pack_supported
+    from phasekv_amd.kernels.packing import quantize_pack
+    print(f"case B={B} H={H} hd={hd} hot_len={hot_len} aged={aged} keep={keep} bits={bits} "
+          f"gs={gs}", flush=True)
+    rng = np.random.default_rng(hd * 7 + keep * 3 + bits)
+    k = (rng.standard_normal((B, H, cap, hd)) * 2).astype(np.float16)
+    v = rng.standard_normal((B, H, cap, hd)).astype(np.float16)
+    hk, hv = torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu)
+    fused = cool_pack_supported(hk, hv, hot_len, aged, keep, gs)
+    assert fused == (hd != 256)
+    seg, idx = cool_pack_hot(hk, hv, hot_len, aged, keep, bits, gs, with_index=True)
+    if keep < aged:
+        want_idx = co.select_kept(co.value_norms(v[:, :, :aged]), keep)
+    else:
+        want_idx = np.broadcast_to(np.arange(aged), (B, H, aged))
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    kept_k = np.take_along_axis(k[:, :, :aged], want_idx[..., None], axis=2)
+    kept_v = np.take_along_axis(v[:, :, :aged], want_idx[..., None], axis=2)
+    for pt, x, axis in ((seg.key, kept_k, -2), (seg.value, kept_v, -1)):
+        want = po.quantize_pack(x, bits, axis, gs)
+        assert pt.group_size == want.group_size and tuple(pt.orig_shape) == want.orig_shape
+        assert np.array_equal(pt.packed.cpu().numpy(), want.packed), axis
+        assert np.array_equal(_u16(pt.scale), want.scale.view(np.int16)), axis
+        assert np.array_equal(_u16(pt.mins), want.mins.view(np.int16)), axis
+        # the same shapes and strides as quantize_pack gives
+        ref = quantize_pack(torch.from_numpy(np.ascontiguousarray(x)).to(gpu), bits, axis, gs)
+        for name in ("packed", "scale", "mins"):
+            a, b = getattr(pt, name), getattr(ref, name)
+            assert a.shape == b.shape and a.stride() == b.stride(), (axis, name)
+    rem = hot_len - aged
+    assert np.array_equal(_u16(hk[:, :, :rem]), k[:, :, aged:hot_len].view(np.int16))
+    assert np.array_equal(_u16(hv[:, :, :rem]), v[:, :, aged:hot_len].view(np.int16))
