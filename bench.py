@@ -1,7 +1,7 @@
 """Benchmark of the PhaseKV Stage-B decode attention on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-sweep] [--no-cpu]
-                    [--no-dense] [--copy-probe-mib M]
+                    [--no-dense] [--copy-probe-mib M] [--lifecycle]
 
 A step is one decode-attention call (one layer, one query token) over the
 packed prompt tier, the cold tier and the FP16 hot window of the workload.
@@ -285,6 +285,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-dense", action="store_true", help="skip the FP16 dense comparator")
+    ap.add_argument("--lifecycle", action="store_true",
+                    help="time only the hot window lifecycle (append, cooling) and print its line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run plain copies of this size (PMC calibration)")
     args = ap.parse_args()
@@ -300,6 +302,18 @@ def main() -> int:
     device = torch.device("cuda:0")
     stream = torch.cuda.Stream(device)
     cfg = workloads.CONFIGS[args.config]
+    if args.lifecycle:
+        rows = []
+        for name, ratio in (("C2", 1.0), ("C2", 0.5), ("C5", 0.5)):
+            r = _bench_lifecycle(workloads.CONFIGS[name], device, min(args.steps, 128),
+                                 min(args.warmup, 128), stream, ratio, not args.no_cpu)
+            rows.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+        print(json.dumps({"metric": "hot window lifecycle: µs per layer-step (append + cooling "
+                                    "event / lazy_g)", "value": rows[0]["us_per_layer_step"],
+                          "unit": "µs", "higher_is_better": False, "n_gpus": 1,
+                          "config": {"workload": "C2 cache shape, keep all"}, "rows": rows}),
+              flush=True)
+        return 0
     if args.copy_probe_mib > 0:
         _copy_probe(args.copy_probe_mib, device)
     _log(f"bench: {cfg} steps={args.steps} warmup={args.warmup}")
