@@ -17,11 +17,14 @@ decode loop:
 * accessors ``__len__``, ``layer_tiers``, ``get_seq_length``, ``get_max_cache_shape``,
   ``true_seq_length``, ``physical_nbytes`` (``:265-289``, ``:436-445``)
 
-``update`` refuses dense use as the reference does (``:447-452``).  Multi-turn
-prompt chunks (``begin_prompt_chunk`` / ``append_prompt_token`` /
-``finish_prompt_chunk``, ``:342-403``) and ``reorder_cache`` (``:454-478``) are not
-part of this module; ``prompt_chunk_len`` is always 0.  The class does not derive
-from ``transformers.cache_utils.Cache``: it is driven by the decode loop directly.
+* multi-turn prompt chunks ``begin_prompt_chunk`` / ``append_prompt_token`` /
+  ``finish_prompt_chunk`` (``:342-403``): the chunk borrows the hot window, and is packed
+  with ``prompt_bits`` into a prompt extension at its end
+* ``reorder_cache`` (``:454-478``): batch reorder of every tier, keeping the transposed
+  K storage ``quantize_pack`` gives
+
+``update`` refuses dense use as the reference does (``:447-452``).  The class does not
+derive from ``transformers.cache_utils.Cache``: it is driven by the decode loop directly.
 """
 from __future__ import annotations
 
@@ -187,6 +190,9 @@ class PhaseKVCache:
         self.lazy_g = lazy_g
         self.decode_keep_ratio = decode_keep_ratio
         self._pending_layers: set = set()
+        # 0: no prompt chunk open; else its length, and every layer's hot_len at its start
+        self._prompt_chunk_len = 0
+        self._prompt_chunk_start: list = []
 
     @classmethod
     @torch.no_grad()
@@ -285,7 +291,7 @@ class PhaseKVCache:
 
     @property
     def prompt_chunk_len(self) -> int:
-        return 0
+        return self._prompt_chunk_len
 
     def physical_nbytes(self) -> int:
         """Bytes of the KV tensors held, hot capacity included."""
@@ -306,10 +312,19 @@ class PhaseKVCache:
     @torch.no_grad()
     def append_hot(self, layer_idx: int, key: torch.Tensor, value: torch.Tensor) -> None:
         """Write this step's rotated K and its V (``[B, Hkv, 1, hd]`` fp16) for one layer."""
+        if self._prompt_chunk_len:
+            raise RuntimeError("a prompt chunk is open: append with append_prompt_token() and "
+                               "close it with finish_prompt_chunk()")
         layer = self.layer_tiers(layer_idx)
         if layer_idx in self._pending_layers:
             raise RuntimeError(f"layer {layer_idx} already appended in this decode step; call "
                                "finish_decode_step() after the forward pass")
+        self._append_token(layer_idx, layer, key, value)
+        self._pending_layers.add(layer_idx)
+
+    def _append_token(self, layer_idx: int, layer: LayerTiers, key: torch.Tensor,
+                      value: torch.Tensor) -> None:
+        """One token into the window (``phasekv_cache.py:405-422``); checks before any write."""
         context = f"layer {layer_idx} new K/V"
         if not isinstance(key, torch.Tensor) or not isinstance(value, torch.Tensor):
             raise TypeError(f"{context} must be tensors")
@@ -337,11 +352,13 @@ class PhaseKVCache:
                                      layer.hot_len, hk.shape[2], _lib.stream_ptr(hk.device)),
                    "append_hot")
         layer.hot_len += 1
-        self._pending_layers.add(layer_idx)
 
     @torch.no_grad()
     def finish_decode_step(self) -> None:
         """After the forward pass of one token: cool every layer, advance the true length."""
+        if self._prompt_chunk_len:
+            raise RuntimeError("a prompt chunk is open: call finish_prompt_chunk(), not "
+                               "finish_decode_step()")
         missing = sorted(set(range(len(self.layers))) - self._pending_layers)
         if missing:
             raise RuntimeError(f"finish_decode_step() needs one appended token per layer; "
@@ -365,3 +382,111 @@ class PhaseKVCache:
                                    self.cold_bits, self.group_size)
         layer.cold.append(segment)
         layer.hot_len -= aged
+
+    # ---- multi-turn prompt chunks -------------------------------------------
+    def _require_idle(self, operation: str) -> None:
+        if self._prompt_chunk_len:
+            raise RuntimeError(f"{operation} cannot run inside a prompt chunk; call "
+                               "finish_prompt_chunk() first")
+        if self._pending_layers:
+            raise RuntimeError(f"{operation} cannot run inside a decode step; layers "
+                               f"{sorted(self._pending_layers)} appended, call finish_decode_step()")
+
+    @staticmethod
+    def _empty_hot(layer: LayerTiers, capacity: int):
+        shape = (*layer.hot_k.shape[:2], capacity, layer.hot_k.shape[-1])
+        return layer.hot_k.new_empty(shape), layer.hot_v.new_empty(shape)
+
+    @torch.no_grad()
+    def begin_prompt_chunk(self, length: int) -> None:
+        """Reserve window rows for a new input chunk of ``length`` tokens (between steps)."""
+        _require_positive_int("length", length)
+        self._require_idle("begin_prompt_chunk()")
+        for layer in self.layers:
+            needed = layer.hot_len + length
+            if needed <= layer.hot_k.shape[2]:
+                continue
+            new_k, new_v = self._empty_hot(layer, needed)
+            new_k[:, :, :layer.hot_len].copy_(layer.hot_k[:, :, :layer.hot_len])
+            new_v[:, :, :layer.hot_len].copy_(layer.hot_v[:, :, :layer.hot_len])
+            layer.hot_k, layer.hot_v = new_k, new_v
+        self._prompt_chunk_start = [layer.hot_len for layer in self.layers]
+        self._prompt_chunk_len = length
+
+    @torch.no_grad()
+    def append_prompt_token(self, layer_idx: int, key: torch.Tensor, value: torch.Tensor) -> None:
+        """One chunk token for one layer; its attention then sees no later chunk token."""
+        if not self._prompt_chunk_len:
+            raise RuntimeError("no prompt chunk is open; call begin_prompt_chunk(length) first")
+        layer = self.layer_tiers(layer_idx)
+        written = layer.hot_len - self._prompt_chunk_start[layer_idx]
+        if written >= self._prompt_chunk_len:
+            raise RuntimeError(f"layer {layer_idx} already holds the chunk's "
+                               f"{self._prompt_chunk_len} tokens")
+        self._append_token(layer_idx, layer, key, value)
+
+    @torch.no_grad()
+    def finish_prompt_chunk(self) -> None:
+        """Pack every chunk token with ``prompt_bits`` into a new prompt extension.
+
+        The generated tokens that were in the window before the chunk stay there as
+        FP16; their cooling is still decided by ``finish_decode_step``.
+        """
+        if not self._prompt_chunk_len:
+            raise RuntimeError("no prompt chunk is open; call begin_prompt_chunk(length) first")
+        for layer_idx, (layer, start) in enumerate(zip(self.layers, self._prompt_chunk_start)):
+            written = layer.hot_len - start
+            if written != self._prompt_chunk_len:
+                raise RuntimeError(f"layer {layer_idx} holds {written} of the chunk's "
+                                   f"{self._prompt_chunk_len} tokens")
+        for layer, start in zip(self.layers, self._prompt_chunk_start):
+            segment = pack_kv(layer.hot_k[:, :, start:layer.hot_len],
+                              layer.hot_v[:, :, start:layer.hot_len],
+                              self.prompt_bits, self.group_size)
+            hot_k, hot_v = self._empty_hot(layer, self.recent_window + self.lazy_g)
+            hot_k[:, :, :start].copy_(layer.hot_k[:, :, :start])
+            hot_v[:, :, :start].copy_(layer.hot_v[:, :, :start])
+            layer.prompt_extensions.append(segment)
+            layer.hot_k, layer.hot_v = hot_k, hot_v
+            layer.hot_len = start
+        self._seen_tokens += self._prompt_chunk_len
+        self._prompt_chunk_len = 0
+        self._prompt_chunk_start = []
+
+    # ---- beam reorder ---------------------------------------------------------
+    @torch.no_grad()
+    def reorder_cache(self, beam_idx: torch.Tensor) -> None:
+        """Reorder the batch of every tier between steps (``phasekv_cache.py:454-478``)."""
+        self._require_idle("reorder_cache()")
+        if (not isinstance(beam_idx, torch.Tensor) or beam_idx.ndim != 1
+                or beam_idx.dtype != torch.long or beam_idx.numel() == 0):
+            raise ValueError("beam_idx must be a non-empty 1-D torch.long tensor")
+        for layer_idx, layer in enumerate(self.layers):
+            if bool((beam_idx < 0).any()) or bool((beam_idx >= layer.hot_k.shape[0]).any()):
+                raise ValueError(f"beam_idx outside layer {layer_idx}'s batch range "
+                                 f"[0, {layer.hot_k.shape[0]})")
+
+        def select(t: torch.Tensor) -> torch.Tensor:
+            index = beam_idx.to(t.device)
+            base = t.transpose(-1, -2)
+            if t.dim() >= 2 and not t.is_contiguous() and base.is_contiguous():
+                # the transposed storage of per-channel K: reorder it and view it back
+                return base.index_select(0, index).transpose(-1, -2)
+            return t.index_select(0, index)
+
+        def reorder(pt: PackedTensor) -> PackedTensor:
+            return PackedTensor(packed=select(pt.packed), scale=select(pt.scale),
+                                mins=select(pt.mins), bits=pt.bits, axis=pt.axis,
+                                group_size=pt.group_size,
+                                orig_shape=(beam_idx.numel(), *tuple(pt.orig_shape)[1:]),
+                                axis_len=pt.axis_len)
+
+        def reorder_segment(seg: PackedKVSegment) -> PackedKVSegment:
+            return PackedKVSegment(reorder(seg.key), reorder(seg.value))
+
+        for layer in self.layers:
+            layer.prompt = reorder_segment(layer.prompt)
+            layer.prompt_extensions = [reorder_segment(s) for s in layer.prompt_extensions]
+            layer.cold = [reorder_segment(s) for s in layer.cold]
+            layer.hot_k = layer.hot_k.index_select(0, beam_idx.to(layer.hot_k.device))
+            layer.hot_v = layer.hot_v.index_select(0, beam_idx.to(layer.hot_v.device))

@@ -221,3 +221,91 @@ def test_cool_pack_hot_matches_cool_then_quantize(gpu, B, H, hd, cap, hot_len, a
     rem = hot_len - aged
     assert np.array_equal(_u16(hk[:, :, :rem]), k[:, :, aged:hot_len].view(np.int16))
     assert np.array_equal(_u16(hv[:, :, :rem]), v[:, :, aged:hot_len].view(np.int16))
+
+
+def test_prompt_chunk_packs_an_extension_and_restores_the_window(gpu):
+    """A 40-token input chunk on a cache whose window holds 20 generated tokens: the window
+    grows for the chunk, the chunk is packed with prompt_bits into a prompt extension equal
+    to the oracle's quantize_pack, the 20 generated tokens stay as FP16, and the decode
+    over the result matches the oracle."""
+    from phasekv_amd.cache import PhaseKVCache
+    from phasekv_amd.kernels.attention_triton import fused_phasekv_decode
+    g = torch.Generator().manual_seed(11)
+    B, H, hq, hd, S, L = 1, 2, 8, 64, 96, 2
+    keys = [torch.randn(B, H, S, hd, generator=g).to(torch.float16) for _ in range(L)]
+    cache = PhaseKVCache.from_dense_prefill(_Dense([k.to(gpu) for k in keys],
+                                                   [(k * 0.5).to(gpu) for k in keys]),
+                                            prompt_len=S, prompt_bits=4, cold_bits=2)
+    gen = []
+    for step in range(20):
+        toks = [(torch.randn(B, H, 1, hd, generator=g).to(torch.float16)) for _ in range(L)]
+        for l in range(L):
+            cache.append_hot(l, toks[l].to(gpu), (toks[l] * 2).to(gpu))
+        cache.finish_decode_step()
+        gen.append(toks)
+    chunk = [torch.randn(B, H, 40, hd, generator=g).to(torch.float16) for _ in range(L)]
+    cache.begin_prompt_chunk(40)
+    assert cache.prompt_chunk_len == 40
+    with pytest.raises(RuntimeError, match="prompt chunk is open"):
+        cache.append_hot(0, chunk[0][:, :, :1].to(gpu), chunk[0][:, :, :1].to(gpu))
+    for t in range(40):
+        for l in range(L):
+            x = chunk[l][:, :, t:t + 1].to(gpu)
+            cache.append_prompt_token(l, x, -x)
+    with pytest.raises(RuntimeError, match="already holds"):
+        cache.append_prompt_token(0, x, x)
+    cache.finish_prompt_chunk()
+    assert cache.prompt_chunk_len == 0 and cache.true_seq_length == S + 20 + 40
+    q = torch.randn(hq, hd, generator=g).to(torch.float16)
+    for l in range(L):
+        tiers = cache.layer_tiers(l)
+        assert tiers.hot_len == 20 and tiers.hot_k.shape[2] == 48 and len(tiers.prompt_extensions) == 1
+        ext = tiers.prompt_extensions[0]
+        wk = po.quantize_pack(chunk[l].numpy(), 4, -2, 32)
+        wv = po.quantize_pack((-chunk[l]).numpy(), 4, -1, 32)
+        for pt, want in ((ext.key, wk), (ext.value, wv)):
+            assert np.array_equal(pt.packed.cpu().numpy(), want.packed)
+            assert np.array_equal(_u16(pt.scale), want.scale.view(np.int16))
+        hot_k, _ = tiers.hot_views()
+        want_hot = torch.cat([t[l] for t in gen], dim=2)
+        assert torch.equal(hot_k.cpu(), want_hot)
+        out = fused_phasekv_decode(q.to(gpu), tiers, hq).float().cpu().numpy()
+        pk = po.quantize_pack(keys[l].numpy(), 4, -2, 32)
+        pv = po.quantize_pack((keys[l] * 0.5).numpy(), 4, -1, 32)
+        segs = [(po.dequantize_float(pk)[0], po.dequantize_float(pv)[0]),
+                (po.dequantize_float(wk)[0], po.dequantize_float(wv)[0]),
+                (want_hot[0].numpy(), (want_hot * 2)[0].numpy())]
+        np.testing.assert_allclose(out, ao.segments_attention(q.numpy(), segs, hq),
+                                   atol=2e-3, rtol=1e-2)
+
+
+def test_reorder_cache_keeps_storage_and_rows(gpu):
+    """reorder_cache([2, 0, 0]) on a 3-row batch after cooling: every tier's rows follow
+    beam_idx, K keeps its transposed storage, and each reordered row decodes like the
+    original row it came from."""
+    from phasekv_amd.cache import PhaseKVCache
+    from phasekv_amd.kernels.attention_triton import fused_phasekv_decode_batched
+    g = torch.Generator().manual_seed(5)
+    B, H, hq, hd, S = 3, 2, 4, 64, 70
+    k = torch.randn(B, H, S, hd, generator=g).to(torch.float16).to(gpu)
+    cache = PhaseKVCache.from_dense_prefill(_Dense([k], [k.flip(-1)]), prompt_len=S,
+                                            decode_keep_ratio=0.5)
+    for step in range(50):
+        t = torch.randn(B, H, 1, hd, generator=g).to(torch.float16).to(gpu)
+        cache.append_hot(0, t, t * 3)
+        cache.finish_decode_step()
+    tiers = cache.layer_tiers(0)
+    assert len(tiers.cold) == 1
+    q = torch.randn(B, hq, hd, generator=g).to(torch.float16).to(gpu)
+    before = fused_phasekv_decode_batched(q, tiers, hq)
+    old_cold_k = tiers.cold[0].key.packed.clone()
+    idx = torch.tensor([2, 0, 0], dtype=torch.long, device=gpu)
+    cache.reorder_cache(idx)
+    tiers = cache.layer_tiers(0)
+    assert torch.equal(tiers.cold[0].key.packed, old_cold_k[idx])
+    assert tiers.cold[0].key.packed.transpose(-1, -2).is_contiguous()
+    assert tiers.prompt.key.scale.transpose(-1, -2).is_contiguous()
+    after = fused_phasekv_decode_batched(q[idx], tiers, hq)
+    assert torch.equal(after, before[idx])
+    with pytest.raises(ValueError, match="beam_idx"):
+        cache.reorder_cache(torch.tensor([3], dtype=torch.long, device=gpu))
