@@ -20,8 +20,10 @@ counters read for it, from the committed PMC summary.
 Prints ONE JSON line (rank 0).  Extra fields: ``us_per_step``, the FP16 dense
 GQA-aware comparator on the same tokens, and ``sweep``: the same measurement
 for the context sweep (C3), the batched configurations (C4, C5), C4's
-prefill-side quantize + pack of an 8192 x 4 x 128 K/V block, and the hot window
-lifecycle (append per step, one cooling event) at the C2 and C5 cache shapes.
+prefill-side quantize + pack of an 8192 x 4 x 128 K/V block, the hot window
+lifecycle (append per step, one cooling event) at the C2 and C5 cache shapes, and
+the causal attention of a 16/64/256-token input chunk at the C2 cache against the
+loop of one decode call per chunk token.
 """
 from __future__ import annotations
 
@@ -208,6 +210,37 @@ def _bench_lifecycle(cfg, device, steps, warmup, stream, ratio, with_cpu):
     return res
 
 
+def _bench_prompt_chunk(cfg, device, T, steps, warmup, stream):
+    """A T-token input chunk at ``cfg``'s cache (its packed tiers, 128 generated hot rows
+    and the chunk as the window's last T rows): the one-pass causal chunk attention
+    against the reference adapter's loop of T decode calls (one per chunk token)."""
+    import dataclasses
+    from phasekv_amd import workloads
+    from phasekv_amd.kernels.attention_triton import (fused_phasekv_decode,
+                                                      fused_phasekv_prompt_chunk_attention)
+    wl = workloads.make_workload(cfg, device)
+    gen = torch.Generator().manual_seed(77)
+    shape = (1, cfg.hkv, cfg.hot + T, cfg.hd)
+    hk = torch.randn(*shape, generator=gen).to(torch.float16).to(device)
+    hv = torch.randn(*shape, generator=gen).to(torch.float16).to(device)
+    tiers = dataclasses.replace(wl.tiers, hot_k=hk, hot_v=hv, hot_len=cfg.hot + T)
+    q = torch.randn(T, cfg.hq, cfg.hd, generator=gen).to(torch.float16).to(device)
+    one = _time_graph([lambda: fused_phasekv_prompt_chunk_attention(q, tiers, cfg.hq)], steps,
+                      warmup, stream)
+    views = [dataclasses.replace(tiers, hot_len=cfg.hot + t + 1) for t in range(T)]
+
+    def loop():
+        for t in range(T):
+            fused_phasekv_decode(q[t], views[t], cfg.hq)
+
+    lsec = _time_graph([loop], max(2, steps // 8), max(2, warmup // 8), stream)
+    del wl, tiers, views
+    torch.cuda.empty_cache()
+    return {"config": f"{cfg.name}-prompt-chunk", "chunk_tokens": T, "chunk_us": one * 1e6,
+            "us_per_chunk_token": one * 1e6 / T, "per_token_loop_us": lsec * 1e6,
+            "speedup_vs_loop": lsec / one}
+
+
 def _cpu_baseline(cfg_name: str, budget_s: float = 10.0):
     """The oracle (reference.py semantics in numpy) on host cores, bounded sample."""
     import numpy as np
@@ -335,6 +368,10 @@ def main() -> int:
             r = _bench_lifecycle(workloads.CONFIGS[name], device, min(args.steps, 128),
                                  min(args.warmup, 128), stream, ratio, not args.no_cpu)
             _log(f"bench: lifecycle {r}")
+            sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+        for T in (16, 64, 256):
+            r = _bench_prompt_chunk(workloads.CONFIGS["C2"], device, T, 32, 32, stream)
+            _log(f"bench: prompt chunk {r}")
             sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
     cpu = None
     if not args.no_cpu:

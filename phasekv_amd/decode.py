@@ -61,10 +61,12 @@ class Segment:
 
 
 def packed_segment(key, value, *, batched: bool, splits: int = 0, split_len: int = 0,
-                   seq_lens: Optional[torch.Tensor] = None) -> Segment:
+                   seq_lens: Optional[torch.Tensor] = None,
+                   broadcast: Optional[int] = None) -> Segment:
     """Segment from a K/V pair of ``PackedTensor`` (KIVI or legacy per-token layout).
 
-    ``batched``: orig_shape is [B, Hkv, S, hd] (else [Hkv, S, hd]).
+    ``batched``: orig_shape is [B, Hkv, S, hd] (else [Hkv, S, hd]).  ``broadcast``: an
+    unbatched segment serves every one of this many batch rows (batch stride 0).
     """
     nd = 4 if batched else 3
     if len(key.orig_shape) != nd or tuple(value.orig_shape) != tuple(key.orig_shape):
@@ -79,7 +81,7 @@ def packed_segment(key, value, *, batched: bool, splits: int = 0, split_len: int
     else:
         raise ValueError("K must be packed along tokens (KIVI) or head_dim (per token)")
     shape = tuple(key.orig_shape)
-    batch = shape[0] if batched else 1
+    batch = shape[0] if batched else (broadcast or 1)
     hkv, s_len, hd = shape[-3], shape[-2], shape[-1]
     if s_len <= 0:
         raise ValueError("packed K/V segment is empty")
@@ -119,8 +121,12 @@ def packed_segment(key, value, *, batched: bool, splits: int = 0, split_len: int
 
 
 def fp16_segment(k: torch.Tensor, v: torch.Tensor, *, batched: bool, splits: int = 0,
-                 split_len: int = 0, seq_lens: Optional[torch.Tensor] = None) -> Segment:
-    """Segment over uncompressed fp16 K/V [B, Hkv, S, hd] (or [Hkv, S, hd]), read in place."""
+                 split_len: int = 0, seq_lens: Optional[torch.Tensor] = None,
+                 broadcast: Optional[int] = None) -> Segment:
+    """Segment over uncompressed fp16 K/V [B, Hkv, S, hd] (or [Hkv, S, hd]), read in place.
+
+    ``broadcast``: an unbatched segment serves every one of this many batch rows.
+    """
     nd = 4 if batched else 3
     if k.dim() != nd or k.shape != v.shape:
         raise ValueError("fp16 K/V must share one [B, Hkv, S, hd] (or [Hkv, S, hd]) shape")
@@ -129,7 +135,7 @@ def fp16_segment(k: torch.Tensor, v: torch.Tensor, *, batched: bool, splits: int
     dev = _lib.require_device(k, v)
     if k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride() != v.stride():
         k, v = k.contiguous(), v.contiguous()
-    batch = k.shape[0] if batched else 1
+    batch = k.shape[0] if batched else (broadcast or 1)
     hkv, s_len, hd = k.shape[-3], k.shape[-2], k.shape[-1]
     if s_len <= 0:
         raise ValueError("fp16 segment is empty")

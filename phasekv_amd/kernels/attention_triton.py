@@ -260,6 +260,58 @@ def fused_phasekv_decode_batched(q: torch.Tensor, tiers, num_attention_heads: in
                                              prompt_lens=prompt_lens))
 
 
+def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers,
+                                         num_attention_heads: int) -> torch.Tensor:
+    """Causal attention of a whole input chunk over the packed cache, in one pass.
+
+    q ``[T, Hq, hd]`` fp16 holds the chunk's T queries in token order; the chunk's
+    K/V are the last T rows of the hot window (``PhaseKVCache.append_prompt_token``).
+    Query t attends to every packed segment, the hot rows before the chunk, and the
+    chunk's rows 0..t: what the reference's adapter computes with one decode call per
+    chunk token (``qwen2_attention.py:100-106``, ``phasekv_cache.py:344-371``).
+    Returns ``[T, Hq, hd]`` fp16.
+
+    Two decode launches and one merge: the T queries ride as ``T * Hq`` heads (head
+    ``(kv, g, t)``) over the packed segments and the pre-chunk hot rows, so each KV
+    chunk is read once per 16 query rows; the chunk's own rows are a batch of T over
+    one broadcast segment with ``t + 1`` valid rows for query t; the two unnormalized
+    partials per query row are merged by log-sum-exp.
+    """
+    if q.dim() != 3 or q.shape[1] != num_attention_heads:
+        raise ValueError("q must be [T, Hq, hd] with Hq = num_attention_heads")
+    T, hq, hd = q.shape
+    hot_len = tiers.hot_len
+    if T <= 0 or T > hot_len:
+        raise ValueError(f"the chunk's {T} tokens must be the last rows of the hot window "
+                         f"(hot_len={hot_len})")
+    hot_k, hot_v = tiers.hot_views()
+    if hot_k.shape[0] != 1:
+        raise ValueError("the PhaseKV prompt chunk path takes batch = 1")
+    start = hot_len - T
+    # (a) packed tiers and the pre-chunk hot rows, the T queries as heads (kv, g, t)
+    segs = []
+    for segment in [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]:
+        segs.append(_dec.packed_segment(_remove_batch(segment.key), _remove_batch(segment.value),
+                                        batched=False))
+    if start:
+        segs.append(_dec.fp16_segment(hot_k[0, :, :start], hot_v[0, :, :start], batched=False))
+    q_heads = q.permute(1, 0, 2).reshape(1, hq * T, hd)
+    ma, la, acca = _dec.decode_mlacc(_dec.Problem(q_heads, segs, hq * T))
+    # (b) the chunk's own rows, causal: query t sees rows start .. start + t
+    lens = torch.arange(1, T + 1, dtype=torch.int32, device=q.device)
+    chunk = _dec.fp16_segment(hot_k[0, :, start:], hot_v[0, :, start:], batched=False,
+                              seq_lens=lens, broadcast=T)
+    mb, lb, accb = _dec.decode_mlacc(_dec.Problem(q, [chunk], hq))
+    # rows of (a) in (t, h) order, then the merge
+    ma = ma.view(hq, T).t()
+    la = la.view(hq, T).t()
+    acca = acca.view(hq, T, hd).permute(1, 0, 2)
+    m = torch.stack((ma.reshape(-1), mb), dim=1)
+    l = torch.stack((la.reshape(-1), lb), dim=1)
+    acc = torch.stack((acca.reshape(-1, hd), accb), dim=1)
+    return _dec.merge_partials(m, l, acc, normalize=True).view(T, hq, hd)
+
+
 def dense_fp16_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                       num_attention_heads: int) -> torch.Tensor:
     """GQA-aware FP16 decode attention over uncompressed K/V (the dense comparator).
