@@ -1,7 +1,7 @@
 """Benchmark of the PhaseKV Stage-B decode attention on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-sweep] [--no-cpu]
-                    [--no-dense] [--copy-probe-mib M] [--lifecycle]
+                    [--no-dense] [--copy-probe-mib M] [--lifecycle] [--prefill]
 
 A step is one decode-attention call (one layer, one query token) over the
 packed prompt tier, the cold tier and the FP16 hot window of the workload.
@@ -23,7 +23,8 @@ for the context sweep (C3), the batched configurations (C4, C5), C4's
 prefill-side quantize + pack of an 8192 x 4 x 128 K/V block, the hot window
 lifecycle (append per step, one cooling event) at the C2 and C5 cache shapes, and
 the causal attention of a 16/64/256-token input chunk at the C2 cache against the
-loop of one decode call per chunk token.
+loop of one decode call per chunk token, and the prefill prompt selection of an
+8192-token prompt.
 """
 from __future__ import annotations
 
@@ -241,6 +242,38 @@ def _bench_prompt_chunk(cfg, device, T, steps, warmup, stream):
             "speedup_vs_loop": lsec / one}
 
 
+def _bench_prompt_select(device, steps, warmup, stream, with_cpu):
+    """C4's prefill side, selection: one layer's prompt selection over an 8192-token
+    prompt (Hq 28 / Hkv 4, observation window 64, keep 25 %, 4 sinks, max pooling over
+    7): the votes read the window's 64 rows of every query head's attention (fp16, the
+    only rows the selection reads), then the per-kv-head pooling and top-k."""
+    from phasekv_amd.prompt_tier import select_prompt_indices
+
+    class Cfg:
+        num_key_value_heads, num_attention_heads = 4, 28
+
+    L, w = 8192, 64
+    gen = torch.Generator().manual_seed(1234)
+    attn = torch.softmax(torch.randn(1, 28, w, L, generator=gen) * 3, dim=-1).to(torch.float16)
+    kw = dict(prompt_len=L, model_config=Cfg, prefill_keep_ratio=0.25, sink_tokens=4,
+              obs_window=w, pool_kernel=7, pooling="maxpool")
+    dev_attn = attn.to(device)
+    sec = _time_graph([lambda: select_prompt_indices([dev_attn], **kw)], steps, warmup, stream)
+    nbytes = attn.numel() * 2
+    res = {"config": "C4-prefill-select", "prompt_len": L, "obs_window": w, "us": sec * 1e6,
+           "votes_bytes": nbytes, "gbs": nbytes / sec / 1e9}
+    if with_cpu:
+        from oracle import select_oracle as so
+        a = attn.float().numpy()
+        t0 = time.perf_counter()
+        so.select_prompt_indices([a], num_kv_heads=4, **{k: v for k, v in kw.items()
+                                                         if k != "model_config"})
+        res["cpu_us"] = (time.perf_counter() - t0) * 1e6
+    del dev_attn
+    torch.cuda.empty_cache()
+    return res
+
+
 def _cpu_baseline(cfg_name: str, budget_s: float = 10.0):
     """The oracle (reference.py semantics in numpy) on host cores, bounded sample."""
     import numpy as np
@@ -318,6 +351,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-dense", action="store_true", help="skip the FP16 dense comparator")
+    ap.add_argument("--prefill", action="store_true",
+                    help="time only the prefill side (C4 pack, prompt selection) and print its line")
     ap.add_argument("--lifecycle", action="store_true",
                     help="time only the hot window lifecycle (append, cooling) and print its line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -335,6 +370,16 @@ def main() -> int:
     device = torch.device("cuda:0")
     stream = torch.cuda.Stream(device)
     cfg = workloads.CONFIGS[args.config]
+    if args.prefill:
+        rows = [_bench_prefill_pack(device, min(args.steps, 128), min(args.warmup, 128), stream),
+                _bench_prompt_select(device, 64, 64, stream, not args.no_cpu)]
+        rows = [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+                for r in rows]
+        print(json.dumps({"metric": "prefill side: C4 pack µs and prompt selection µs per layer",
+                          "value": rows[1]["us"], "unit": "µs", "higher_is_better": False,
+                          "n_gpus": 1, "config": {"workload": "C4 prefill"}, "rows": rows}),
+              flush=True)
+        return 0
     if args.lifecycle:
         rows = []
         for name, ratio in (("C2", 1.0), ("C2", 0.5), ("C5", 0.5)):
@@ -369,6 +414,9 @@ def main() -> int:
                                  min(args.warmup, 128), stream, ratio, not args.no_cpu)
             _log(f"bench: lifecycle {r}")
             sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+        r = _bench_prompt_select(device, 64, 64, stream, not args.no_cpu)
+        _log(f"bench: prompt select {r}")
+        sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
         for T in (16, 64, 256):
             r = _bench_prompt_chunk(workloads.CONFIGS["C2"], device, T, 32, 32, stream)
             _log(f"bench: prompt chunk {r}")

@@ -239,6 +239,32 @@ int pk_cool_pack_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride, int6
                      uint8_t* k_packed, uint16_t* k_scale, uint16_t* k_mins, uint8_t* v_packed,
                      uint16_t* v_scale, uint16_t* v_mins, int64_t* out_index, void* stream);
 
+/* ---- prefill prompt selection (src/phasekv/prompt_tier.py) ----------------- */
+
+/* Observation-window votes of one layer: votes[b, kv, j] (fp32 [batch,
+ * num_kv_heads, kv_len] contiguous) = sum over the kv head's query heads (in
+ * order) of the sum over the last min(obs_window, q_len) query rows (in order) of
+ * attention[b, h, row, j], in float32.  attention is [batch, num_q_heads, q_len,
+ * kv_len] of dtype PK_DTYPE_* with element strides strides[4].  Replaces
+ * observation_votes + aggregate_to_kv_heads (src/phasekv/hetero_cache.py:55-77). */
+int pk_prompt_votes(const void* attention, int dtype, int64_t batch, int64_t num_q_heads,
+                    int64_t q_len, int64_t kv_len, const int64_t* strides, int num_kv_heads,
+                    int obs_window, float* votes, void* stream);
+
+/* Kept prompt positions of each of `rows` vote rows (fp32 [rows, kv_len]): the
+ * sink positions [0, sink), then the select_k best candidates of [sink,
+ * recent_start) after 1-D pooling of their votes (pool_mode 0: max over the
+ * window, padding never wins; 1: average with zero padding, divided by
+ * pool_kernel; window = pool_kernel positions starting pool_kernel / 2 before the
+ * candidate; pool_kernel <= 1: no pooling; equal scores: the earlier position;
+ * NaN above every number), then [recent_start, kv_len): int64 keep [rows,
+ * sink + select_k + kv_len - recent_start], ascending.  Replaces the selection of
+ * select_prompt_indices (src/phasekv/prompt_tier.py:43-75) with pool_scores and
+ * topk_per_head (src/phasekv/hetero_cache.py:80-94, 147-157). */
+int pk_select_prompt(const float* votes, int64_t rows, int64_t kv_len, int64_t sink,
+                     int64_t recent_start, int64_t select_k, int pool_kernel, int pool_mode,
+                     int64_t* keep, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,8 @@ HIP kernels in ``phasekv_amd`` implement:
 * ``launch_config_oracle`` — ``src/phasekv/kernels/launch_config.py:6-64``
 * ``cache_oracle``         — the hot window lifecycle of
   ``src/phasekv/phasekv_cache.py:101-114,322-340,405-422``
+* ``select_oracle``        — prefill prompt selection, ``src/phasekv/prompt_tier.py:22-76``
+  and ``src/phasekv/hetero_cache.py:55-94,147-157``
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker.  The product
@@ -33,6 +35,11 @@ Pinning status (what checks each function independently of its own formula):
   float64 norm; ties and NaN by brute force over explicit rankings; the cooled
   segment equals ``quantize_pack`` of the kept rows and the shifted window equals
   slicing; ``keep_count`` against Python's round on half-way cases.
+* select_oracle (votes, pooling, kept positions) — votes, pooling and the kept set
+  equal torch's own ``float().sum``, ``F.max_pool1d`` / ``F.avg_pool1d`` and
+  ``topk().indices`` (the calls the reference makes) on tie-free inputs; the plan
+  against hand-worked budgets; max pooling exact against a brute-force window max;
+  ties and NaN by brute force.
 * plan_kivi_decode — known-answer tests from the reference's
   ``tests/test_phasekv_launch_config.py:10-47`` and the published plan table
   (``docs/idea/PhaseKV-技术原理与系统设计.md:495-502``).

@@ -111,6 +111,11 @@ _SIGNATURES = {
                                         ctypes.c_int, ctypes.c_int, _c_i64, _c_i64, _c_i64,
                                         ctypes.c_int, ctypes.c_int, _c_vp, _c_vp, _c_vp, _c_vp,
                                         _c_vp, _c_vp, _c_vp, _c_vp]),
+    "pk_prompt_votes": (ctypes.c_int, [_c_vp, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64,
+                                       ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_int, _c_vp,
+                                       _c_vp]),
+    "pk_select_prompt": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                        ctypes.c_int, ctypes.c_int, _c_vp, _c_vp]),
 }
 
 _lib = None

@@ -15,7 +15,7 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libphasekv_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["pk_capi.hip", "pk_pack.hip", "pk_decode.hip", "pk_decode_mfma.hip", "pk_cache.hip"]
+SOURCES = ["pk_capi.hip", "pk_pack.hip", "pk_decode.hip", "pk_decode_mfma.hip", "pk_cache.hip", "pk_select.hip"]
 ARCH = "gfx950"
 
 

@@ -1,0 +1,340 @@
+// Prefill-side prompt selection (gfx950): observation-window votes over the
+// prefill attention, GQA aggregation, 1-D pooling of the candidate scores and a
+// per-kv-head top-k, producing the sorted positions the prompt tier keeps.
+//
+// Semantics follow the reference:
+//   select_prompt_indices   src/phasekv/prompt_tier.py:22-76
+//   observation_votes       src/phasekv/hetero_cache.py:67-77
+//   aggregate_to_kv_heads   src/phasekv/hetero_cache.py:55-64
+//   pool_scores             src/phasekv/hetero_cache.py:80-94 (max_pool1d / avg_pool1d,
+//                           stride 1, padding kernel // 2, truncated to the length)
+//   topk_per_head           src/phasekv/hetero_cache.py:147-157
+#include "pk_common.h"
+
+#include <algorithm>
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kSelThreads = 256;
+// candidates whose votes and keys are staged in LDS (8 bytes each, 144 KB)
+constexpr int64_t kMaxStagedKeys = 18 * 1024;
+
+struct AttnView {
+  const void* p;
+  int dtype;
+  int64_t sb, sh, sq, sk;   // element strides of batch, head, query row, key
+};
+
+__device__ __forceinline__ float load_attn(const AttnView& a, int64_t off) {
+  if (a.dtype == PK_DTYPE_F16) return pk_h2f(static_cast<const uint16_t*>(a.p)[off]);
+  if (a.dtype == PK_DTYPE_BF16) return pk_bf2f(static_cast<const uint16_t*>(a.p)[off]);
+  return static_cast<const float*>(a.p)[off];
+}
+
+// votes[b, kv, j] = sum over the group's query heads g (in order) of the sum over
+// the last w query rows r (in order) of attention[b, kv * G + g, q_len - w + r, j],
+// all in float32.  A workgroup takes 64 * KPL key positions of one (b, kv): wave s
+// sums the rows of query heads s, s + 4, ... (KPL neighbouring keys per lane in one
+// load, 8 rows of loads in flight, added in row order), and wave 0 adds the heads'
+// sums in head order.
+constexpr int kMaxGroup = 32;
+
+template <int KPL, typename T>
+__device__ __forceinline__ void load_keys(const AttnView& a, int64_t off, float (&x)[KPL]) {
+  if constexpr (KPL == 1) {
+    x[0] = load_attn(a, off);
+  } else {
+    using V = uint16_t __attribute__((ext_vector_type(KPL)));
+    const V v = *reinterpret_cast<const V*>(static_cast<const uint16_t*>(a.p) + off);
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+      x[i] = a.dtype == PK_DTYPE_F16 ? pk_h2f(v[i]) : pk_bf2f(v[i]);
+  }
+}
+
+template <int KPL>
+__global__ void __launch_bounds__(kSelThreads)
+votes_kernel(AttnView a, int Hkv, int G, int64_t q_len, int64_t kv_len, int w,
+             float* __restrict__ votes) {
+  constexpr int TILE = 64 * KPL;
+  __shared__ float hs[kMaxGroup][TILE];
+  const int lane = threadIdx.x & 63, slot = threadIdx.x >> 6;
+  const int64_t tiles = (kv_len + TILE - 1) / TILE;
+  const int64_t row = blockIdx.x / tiles;                 // b * Hkv + kv
+  const int64_t j0 = (blockIdx.x - row * tiles) * TILE + lane * KPL;
+  const int64_t b = row / Hkv, kv = row - b * Hkv;
+  const int64_t jc = min(j0, kv_len - KPL);               // whole pieces stay inside the row
+  for (int g = slot; g < G; g += kSelThreads / 64) {
+    const int64_t base = b * a.sb + (kv * G + g) * a.sh + (q_len - w) * a.sq + jc * a.sk;
+    float sum[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) sum[i] = 0.f;
+    int r = 0;
+    for (; r + 8 <= w; r += 8) {
+      float x[8][KPL];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) load_keys<KPL, void>(a, base + (r + u) * a.sq, x[u]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) sum[i] = __fadd_rn(sum[i], x[u][i]);
+    }
+    for (; r < w; ++r) {
+      float x[KPL];
+      load_keys<KPL, void>(a, base + r * a.sq, x);
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) sum[i] = __fadd_rn(sum[i], x[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) hs[g][lane * KPL + i] = sum[i];
+  }
+  __syncthreads();
+  if (slot == 0) {
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const int64_t j = j0 + i;
+      if (j >= kv_len || j - jc >= KPL || j < jc) continue;
+      float v = hs[0][lane * KPL + (int)(j - jc)];
+      for (int g = 1; g < G; ++g) v = __fadd_rn(v, hs[g][lane * KPL + (int)(j - jc)]);
+      votes[row * kv_len + j] = v;
+    }
+  }
+}
+
+// Pooled score of candidate j (0 <= j < n) of the row's candidates c[0 .. n):
+// max pooling takes the max over c[j - pad .. j - pad + k - 1] inside [0, n)
+// (padding never wins); average pooling adds the window's values left to right
+// (padding counts as 0) and divides by k.
+__device__ __forceinline__ float pooled(const float* c, int64_t n, int64_t j, int k, int mode) {
+  if (k <= 1) return c[j];
+  const int64_t lo = j - k / 2;
+  if (mode == 0) {
+    float m = -INFINITY;
+    bool nan = false;
+    for (int t = 0; t < k; ++t) {
+      const int64_t x = lo + t;
+      if (x < 0 || x >= n) continue;
+      const float v = c[x];
+      nan |= v != v;
+      m = fmaxf(m, v);
+    }
+    return nan ? __int_as_float(0x7fc00000) : m;
+  }
+  float s = 0.f;
+  for (int t = 0; t < k; ++t) {
+    const int64_t x = lo + t;
+    if (x >= 0 && x < n) s = __fadd_rn(s, c[x]);
+  }
+  return __fdiv_rn(s, (float)k);
+}
+
+// Order-preserving key of a score: larger score, larger key; every NaN above +inf.
+__device__ __forceinline__ uint32_t score_key(float v) {
+  if (v != v) return 0xffffffffu;
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Exclusive prefix sum of v over the workgroup's threads (tid order); uses
+// scratch[kSelThreads / 64] and synchronizes the workgroup.
+__device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* scratch) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int64_t inc = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t u = __shfl_up(inc, o);
+    if (lane >= o) inc += u;
+  }
+  if (lane == 63) scratch[wave] = inc;
+  __syncthreads();
+  int64_t before = 0;
+  for (int w = 0; w < wave; ++w) before += scratch[w];
+  __syncthreads();
+  return before + inc - v;
+}
+
+// Keys of the candidates: in LDS (staged once) when the row fits, else
+// recomputed from the votes in global memory on every pass.
+struct KeySource {
+  const float* c;
+  int64_t n;
+  int pool_k, pool_mode;
+  const uint32_t* lds;   // n keys, or null
+  __device__ __forceinline__ uint32_t operator()(int64_t j) const {
+    return lds ? lds[j] : score_key(pooled(c, n, j, pool_k, pool_mode));
+  }
+};
+
+// One workgroup per (b, kv): sink positions, then the select_k best pooled
+// candidates of [sink, recent_start) (ties: the earlier position), then the
+// recent positions, in ascending order.
+__global__ void __launch_bounds__(kSelThreads)
+select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int64_t recent_start,
+              int64_t select_k, int pool_k, int pool_mode, int64_t* __restrict__ keep,
+              int64_t budget, int staged) {
+  extern __shared__ uint32_t lds_keys[];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_prefix, s_mask, s_need;
+  __shared__ int64_t s_count[kSelThreads / 64];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* c = votes + row * kv_len + sink;
+  const int64_t n = recent_start - sink;
+  int64_t* out = keep + row * budget;
+  for (int64_t i = tid; i < sink; i += kSelThreads) out[i] = i;
+  for (int64_t i = tid; i < kv_len - recent_start; i += kSelThreads)
+    out[sink + select_k + i] = recent_start + i;
+  if (select_k <= 0) return;
+  KeySource key_of{c, n, pool_k, pool_mode, nullptr};
+  if (staged) {
+    // the row's votes into LDS (8 loads in flight per thread), then the keys
+    float* raw = reinterpret_cast<float*>(lds_keys + n);
+    for (int64_t j0 = tid; j0 < n; j0 += 8 * kSelThreads) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t j = j0 + u * kSelThreads;
+        x[u] = j < n ? c[j] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t j = j0 + u * kSelThreads;
+        if (j < n) raw[j] = x[u];
+      }
+    }
+    __syncthreads();
+    for (int64_t j = tid; j < n; j += kSelThreads)
+      lds_keys[j] = score_key(pooled(raw, n, j, pool_k, pool_mode));
+    key_of.lds = lds_keys;
+  }
+  // radix select of the select_k-th largest key, 8 bits at a time from the top
+  if (tid == 0) {
+    s_prefix = 0;
+    s_mask = 0;
+    s_need = (uint32_t)select_k;
+  }
+  __syncthreads();
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[tid] = 0;
+    __syncthreads();
+    const uint32_t prefix = s_prefix, mask = s_mask;
+    for (int64_t j = tid; j < n; j += kSelThreads) {
+      const uint32_t key = key_of(j);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    // suffix sums of the histogram (thread t: keys with digit >= t), then the one
+    // digit d with suffix(d) >= need > suffix(d + 1) is the threshold's digit
+    const uint32_t need = s_need;
+    uint32_t suf = hist[tid];
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t v = __shfl_down(suf, o);
+      if ((tid & 63) + o < 64) suf += v;
+    }
+    __syncthreads();
+    hist[tid] = suf;                       // suffix within the wave
+    __syncthreads();
+    for (int wv = (tid >> 6) + 1; wv < kSelThreads / 64; ++wv) suf += hist[wv * 64];
+    __syncthreads();
+    hist[tid] = suf;                       // full suffix sums
+    __syncthreads();
+    const uint32_t next = tid < 255 ? hist[tid + 1] : 0u;
+    if (suf >= need && next < need) {
+      s_prefix = prefix | ((uint32_t)tid << shift);
+      s_mask = mask | (255u << shift);
+      s_need = need - next;
+    }
+    __syncthreads();
+  }
+  // the threshold key and how many candidates equal to it are kept (the earliest)
+  const uint32_t thr = s_prefix;
+  const int64_t take_equal = s_need;
+  // each thread scans one contiguous range: counts, then a block scan of the
+  // counts gives each thread its first output slot
+  const int64_t per = (n + kSelThreads - 1) / kSelThreads;
+  const int64_t j0 = min<int64_t>(n, tid * per), j1 = min<int64_t>(n, j0 + per);
+  int64_t above = 0, equal = 0;
+  for (int64_t j = j0; j < j1; ++j) {
+    const uint32_t key = key_of(j);
+    above += key > thr;
+    equal += key == thr;
+  }
+  // exclusive prefix of the equal counts decides which equal keys are taken
+  const int64_t eq_before = block_exclusive_scan(equal, s_count);
+  const int64_t eq_take = max<int64_t>(0, min<int64_t>(equal, take_equal - eq_before));
+  int64_t slot = block_exclusive_scan(above + eq_take, s_count);
+  int64_t eq_left = eq_take;
+  for (int64_t j = j0; j < j1; ++j) {
+    const uint32_t key = key_of(j);
+    bool take = key > thr;
+    if (key == thr && eq_left > 0) {
+      take = true;
+      --eq_left;
+    }
+    if (take) out[sink + slot++] = sink + j;
+  }
+}
+
+}  // namespace
+
+extern "C" int pk_prompt_votes(const void* attention, int dtype, int64_t batch, int64_t num_q_heads,
+                               int64_t q_len, int64_t kv_len, const int64_t* strides,
+                               int num_kv_heads, int obs_window, float* votes, void* stream) {
+  pk::clear_error();
+  if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16 && dtype != PK_DTYPE_F32)
+    return pk::fail("attention must be float16, bfloat16 or float32");
+  if (batch <= 0 || num_q_heads <= 0 || q_len <= 0 || kv_len <= 0 || num_kv_heads <= 0)
+    return pk::fail("attention shape and kv heads must be positive");
+  if (num_q_heads % num_kv_heads) return pk::fail("query heads must be a multiple of kv heads");
+  if (obs_window <= 0) return pk::fail("obs_window must be positive");
+  if (!attention || !votes || !strides) return pk::fail("null pointer");
+  if (num_q_heads / num_kv_heads > kMaxGroup) return pk::fail("more than 32 query heads per kv head");
+  const int w = (int)std::min<int64_t>(obs_window, q_len);
+  AttnView a{attention, dtype, strides[0], strides[1], strides[2], strides[3]};
+  const int G = (int)(num_q_heads / num_kv_heads);
+  // 4 keys per lane in one 8-byte load for 16-bit attention with contiguous,
+  // 8-byte aligned key rows of a multiple of 4 keys; else one key per lane
+  const bool vec = dtype != PK_DTYPE_F32 && strides[3] == 1 && kv_len % 4 == 0 &&
+                   strides[0] % 4 == 0 && strides[1] % 4 == 0 && strides[2] % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(attention) % 8 == 0;
+  const int kpl = vec ? 4 : 1;
+  const int64_t blocks = batch * num_kv_heads * pk::cdiv(kv_len, 64 * kpl);
+  if (blocks > 0x7fffffff) return pk::fail("attention too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (vec)
+    hipLaunchKernelGGL(votes_kernel<4>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+                       num_kv_heads, G, q_len, kv_len, w, votes);
+  else
+    hipLaunchKernelGGL(votes_kernel<1>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+                       num_kv_heads, G, q_len, kv_len, w, votes);
+  return pk::check_launch("prompt_votes");
+}
+
+extern "C" int pk_select_prompt(const float* votes, int64_t rows, int64_t kv_len, int64_t sink,
+                                int64_t recent_start, int64_t select_k, int pool_kernel,
+                                int pool_mode, int64_t* keep, void* stream) {
+  pk::clear_error();
+  if (rows <= 0 || kv_len <= 0) return pk::fail("rows and kv_len must be positive");
+  if (sink < 0 || recent_start < sink || recent_start > kv_len)
+    return pk::fail("need 0 <= sink <= recent_start <= kv_len");
+  if (select_k < 0 || select_k > recent_start - sink)
+    return pk::fail("select_k must lie in [0, recent_start - sink]");
+  if (pool_mode != 0 && pool_mode != 1) return pk::fail("pool_mode must be 0 (max) or 1 (avg)");
+  if (!votes || !keep) return pk::fail("null pointer");
+  const int64_t budget = sink + select_k + (kv_len - recent_start);
+  const int64_t n = recent_start - sink;
+  const int staged = n <= kMaxStagedKeys ? 1 : 0;
+  const size_t lds = staged ? (size_t)n * 8 : 0;
+  static bool lds_opt_in = [] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(kMaxStagedKeys * 8)) == hipSuccess;
+  }();
+  if (staged && lds > 64 * 1024 && !lds_opt_in)
+    return pk::fail("cannot reserve the selection kernel's LDS"), PK_ERR_RUNTIME;
+  hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(kSelThreads), lds,
+                     static_cast<hipStream_t>(stream), votes, kv_len, sink, recent_start,
+                     select_k, pool_kernel, pool_mode, keep, budget, staged);
+  return pk::check_launch("select_prompt");
+}
