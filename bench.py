@@ -1,7 +1,7 @@
 """Benchmark of the PhaseKV Stage-B decode attention on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-sweep] [--no-cpu]
-                    [--no-dense] [--copy-probe-mib M] [--lifecycle] [--prefill]
+                    [--no-dense] [--copy-probe-mib M] [--lifecycle] [--prefill] [--e2e]
 
 A step is one decode-attention call (one layer, one query token) over the
 packed prompt tier, the cold tier and the FP16 hot window of the workload.
@@ -274,6 +274,49 @@ def _bench_prompt_select(device, steps, warmup, stream, with_cpu):
     return res
 
 
+def _bench_e2e(device, prompt_len, layers, steps):
+    """Time per output token of a random-weight Qwen2.5-7B-shaped model (``layers`` of its
+    28 decoder layers, fp16) decoding after a ``prompt_len``-token prefill: the PhaseKV
+    adapter (2-bit prompt, 4-bit cold, FP16 window of 32 + 16) against the model's own
+    dense DynamicCache decode with SDPA, both in eager mode (the same Python overhead)."""
+    from transformers import DynamicCache, Qwen2Config, Qwen2ForCausalLM
+    from phasekv_amd.qwen2_attention import (install_qwen2_phasekv_attention, phasekv_prefill,
+                                             phasekv_step)
+    cfg = Qwen2Config(vocab_size=152064, hidden_size=3584, intermediate_size=18944,
+                      num_hidden_layers=layers, num_attention_heads=28, num_key_value_heads=4,
+                      max_position_embeddings=32768, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    with torch.device(device):
+        model = Qwen2ForCausalLM(cfg).half().eval()
+    install_qwen2_phasekv_attention(model)
+    gen = torch.Generator().manual_seed(1234)
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=gen).to(device)
+    toks = torch.randint(0, cfg.vocab_size, (steps + 8, 1), generator=gen).to(device)
+    with torch.no_grad():
+        _, cache = phasekv_prefill(model, prompt, prompt_bits=2, cold_bits=4)
+        dense = DynamicCache(config=cfg)
+        model(prompt, past_key_values=dense, use_cache=True)
+        for i in range(8):
+            phasekv_step(model, toks[i:i + 1], cache)
+            model(toks[i:i + 1], past_key_values=dense, use_cache=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(8, 8 + steps):
+            phasekv_step(model, toks[i:i + 1], cache)
+        torch.cuda.synchronize()
+        pk = (time.perf_counter() - t0) / steps
+        t0 = time.perf_counter()
+        for i in range(8, 8 + steps):
+            model(toks[i:i + 1], past_key_values=dense, use_cache=True)
+        torch.cuda.synchronize()
+        dn = (time.perf_counter() - t0) / steps
+    del model, cache, dense
+    torch.cuda.empty_cache()
+    return {"config": f"e2e-qwen2.5-7b-shape-{layers}L", "prompt_len": prompt_len,
+            "phasekv_ms_per_token": pk * 1e3, "dense_ms_per_token": dn * 1e3,
+            "speedup_vs_dense": dn / pk}
+
+
 def _cpu_baseline(cfg_name: str, budget_s: float = 10.0):
     """The oracle (reference.py semantics in numpy) on host cores, bounded sample."""
     import numpy as np
@@ -351,6 +394,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-dense", action="store_true", help="skip the FP16 dense comparator")
+    ap.add_argument("--e2e", action="store_true",
+                    help="time per output token of the Qwen2 adapter against the dense cache")
     ap.add_argument("--prefill", action="store_true",
                     help="time only the prefill side (C4 pack, prompt selection) and print its line")
     ap.add_argument("--lifecycle", action="store_true",
@@ -370,6 +415,17 @@ def main() -> int:
     device = torch.device("cuda:0")
     stream = torch.cuda.Stream(device)
     cfg = workloads.CONFIGS[args.config]
+    if args.e2e:
+        rows = [_bench_e2e(device, L, 4, 32) for L in (4096, 16384, 32768)]
+        rows = [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+                for r in rows]
+        print(json.dumps({"metric": "time per output token, Qwen2.5-7B-shaped random-weight "
+                                    "model (4 of 28 layers), PhaseKV adapter vs dense cache",
+                          "value": rows[0]["phasekv_ms_per_token"], "unit": "ms",
+                          "higher_is_better": False, "n_gpus": 1,
+                          "config": {"workload": "Qwen2.5-7B shape, 4 layers, fp16"},
+                          "rows": rows}), flush=True)
+        return 0
     if args.prefill:
         rows = [_bench_prefill_pack(device, min(args.steps, 128), min(args.warmup, 128), stream),
                 _bench_prompt_select(device, 64, 64, stream, not args.no_cpu)]

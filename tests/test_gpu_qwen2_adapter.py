@@ -1,0 +1,77 @@
+"""The Qwen2 adapter end to end on a small random-weight Qwen2 (transformers 5.x): PhaseKV
+decode steps and an input chunk against the model's own dense DynamicCache decode on the
+same tokens, and a prefill with prompt selection."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(gpu, attn="sdpa", layers=2):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    cfg = Qwen2Config(vocab_size=2000, hidden_size=512, intermediate_size=1024,
+                      num_hidden_layers=layers, num_attention_heads=8, num_key_value_heads=2,
+                      max_position_embeddings=8192, attn_implementation=attn)
+    torch.manual_seed(0)
+    with torch.device(gpu):
+        model = Qwen2ForCausalLM(cfg)
+    for p in model.parameters():           # wider weights than the default init, so the
+        p.data.normal_(0.0, 0.06)          # logits spread and small errors would show
+    return model.half().eval()
+
+
+def _close(a, b):
+    a, b = a.float().flatten(), b.float().flatten()
+    cos = torch.nn.functional.cosine_similarity(a, b, dim=0).item()
+    rel = ((a - b).abs().max() / b.abs().max()).item()
+    return cos, rel
+
+
+@torch.no_grad()
+def test_decode_and_chunk_match_the_dense_cache(gpu):
+    from transformers import DynamicCache
+    from phasekv_amd.qwen2_attention import (install_qwen2_phasekv_attention, phasekv_prefill,
+                                             phasekv_step)
+    model = _model(gpu)
+    install_qwen2_phasekv_attention(model)
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, 2000, (1, 300), generator=g).to(gpu)
+    first, cache = phasekv_prefill(model, prompt, prompt_bits=8, cold_bits=8, recent_window=32,
+                                   lazy_g=16)
+    dense = DynamicCache(config=model.config)
+    ref = model(prompt, past_key_values=dense, use_cache=True).logits[:, -1]
+    assert torch.equal(first, ref)                      # the prefill itself is the model's
+    tok = ref.argmax(-1, keepdim=True)
+    worst = 1.0
+    for step in range(60):
+        mine = phasekv_step(model, tok, cache)
+        want = model(tok, past_key_values=dense, use_cache=True).logits[:, -1]
+        cos, rel = _close(mine, want)
+        worst = min(worst, cos)
+        assert cos > 0.999 and rel < 0.05, (step, cos, rel)
+        tok = want.argmax(-1, keepdim=True)
+    tiers = cache.layer_tiers(0)
+    assert len(tiers.cold) == 1 and cache.true_seq_length == 360
+    # a new 12-token input chunk, attended in one pass per layer
+    chunk = torch.randint(0, 2000, (1, 12), generator=g).to(gpu)
+    mine = phasekv_step(model, chunk, cache)
+    want = model(chunk, past_key_values=dense, use_cache=True).logits[:, -1]
+    cos, rel = _close(mine, want)
+    assert cos > 0.999 and rel < 0.05, (cos, rel)
+    assert cache.true_seq_length == 372 and len(cache.layer_tiers(1).prompt_extensions) == 1
+    print(f"worst decode cosine {worst:.6f}")
+
+
+@torch.no_grad()
+def test_prefill_with_prompt_selection(gpu):
+    from phasekv_amd.qwen2_attention import (install_qwen2_phasekv_attention, phasekv_prefill,
+                                             phasekv_step)
+    model = _model(gpu, attn="eager")
+    install_qwen2_phasekv_attention(model)
+    prompt = torch.randint(0, 2000, (1, 256), generator=torch.Generator().manual_seed(2)).to(gpu)
+    _, cache = phasekv_prefill(model, prompt, prefill_keep_ratio=0.5, sink_tokens=4,
+                               obs_window=32, pool_kernel=7)
+    assert cache.layer_tiers(0).prompt.length == 128 and cache.true_seq_length == 256
+    logits = phasekv_step(model, prompt[:, -1:], cache)
+    assert torch.isfinite(logits).all() and cache.true_seq_length == 257
