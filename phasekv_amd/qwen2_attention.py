@@ -26,21 +26,24 @@ from .kernels.attention_triton import (fused_phasekv_decode,
 from .prompt_tier import select_prompt_indices
 
 
-def _apply_rope(q, k, cos, sin):
-    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
-    return apply_rotary_pos_emb(q, k, cos, sin)
-
-
-class PhaseKVQwen2Attention(nn.Module):
+class PhaseKVAttention(nn.Module):
     """Reuses the wrapped attention's projections; handles single-token decode and input
     chunks on a ``PhaseKVCache``.  The layer only writes K/V and attends; the caller
-    calls ``finish_decode_step`` / ``finish_prompt_chunk`` after the model's forward."""
+    calls ``finish_decode_step`` / ``finish_prompt_chunk`` after the model's forward.
+    Subclasses give the model family's RoPE."""
 
     def __init__(self, original: nn.Module):
         super().__init__()
         self.original = original
         self.layer_idx = original.layer_idx
         self.train(original.training)
+
+    @staticmethod
+    def rope(q, k, cos, sin):
+        raise NotImplementedError
+
+    def check(self) -> None:
+        """Model-family conditions of the PhaseKV path."""
 
     def forward(self, hidden_states, position_embeddings=None, attention_mask=None,
                 past_key_values=None, **kwargs):
@@ -49,9 +52,10 @@ class PhaseKVQwen2Attention(nn.Module):
                                  past_key_values=past_key_values, **kwargs)
         batch, q_len, _ = hidden_states.shape
         if batch != 1 or hidden_states.dtype not in (torch.float16, torch.bfloat16):
-            raise ValueError("PhaseKV Qwen2 takes batch = 1 in float16 / bfloat16")
+            raise ValueError("the PhaseKV attention takes batch = 1 in float16 / bfloat16")
         if self.training:
             raise ValueError("PhaseKV decode needs eval()")
+        self.check()
         cache = past_key_values
         if cache.prompt_chunk_len:
             if q_len != cache.prompt_chunk_len:
@@ -69,7 +73,7 @@ class PhaseKVQwen2Attention(nn.Module):
         if position_embeddings is None:
             raise ValueError("position_embeddings (RoPE cos, sin at the true positions) are needed")
         cos, sin = position_embeddings
-        q, k = _apply_rope(q, k, cos, sin)
+        q, k = self.rope(q, k, cos, sin)
         q, k, v = q.to(torch.float16), k.to(torch.float16), v.to(torch.float16)
         tiers = cache.layer_tiers(self.layer_idx)
         if cache.prompt_chunk_len:
@@ -81,6 +85,15 @@ class PhaseKVQwen2Attention(nn.Module):
             out = fused_phasekv_decode(q[0, :, 0, :], tiers, hq).unsqueeze(0)
         out = out.reshape(batch, q_len, hq * hd).to(hidden_states.dtype)
         return base.o_proj(out), None
+
+
+class PhaseKVQwen2Attention(PhaseKVAttention):
+    """``PhaseKVQwen2Attention`` of ``qwen2_attention.py:19-109``."""
+
+    @staticmethod
+    def rope(q, k, cos, sin):
+        from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+        return apply_rotary_pos_emb(q, k, cos, sin)
 
 
 def install_qwen2_phasekv_attention(model) -> int:
@@ -136,8 +149,11 @@ def phasekv_step(model, input_ids: torch.Tensor, cache: PhaseKVCache) -> torch.T
         cache.begin_prompt_chunk(T)
     start = cache.true_seq_length
     pos = torch.arange(start, start + T, device=input_ids.device).unsqueeze(0)
-    masks = {t: None for t in set(model.config.layer_types)}
-    out = model(input_ids, position_ids=pos, past_key_values=cache, attention_mask=masks,
+    # a 4-D mask is passed through as is: transformers builds no mask and asks the
+    # cache nothing (the PhaseKV attention ignores the mask; causality comes from the
+    # append order and the chunk attention)
+    mask = torch.zeros(1, 1, T, 1, dtype=torch.bool, device=input_ids.device)
+    out = model(input_ids, position_ids=pos, past_key_values=cache, attention_mask=mask,
                 use_cache=True)
     if T > 1:
         cache.finish_prompt_chunk()

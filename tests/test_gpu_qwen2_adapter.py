@@ -75,3 +75,35 @@ def test_prefill_with_prompt_selection(gpu):
     assert cache.layer_tiers(0).prompt.length == 128 and cache.true_seq_length == 256
     logits = phasekv_step(model, prompt[:, -1:], cache)
     assert torch.isfinite(logits).all() and cache.true_seq_length == 257
+
+
+@torch.no_grad()
+def test_llama_adapter_matches_the_dense_cache(gpu):
+    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
+    from phasekv_amd.llama_attention import (install_llama_phasekv_attention, phasekv_prefill,
+                                             phasekv_step)
+    cfg = LlamaConfig(vocab_size=2000, hidden_size=512, intermediate_size=1024,
+                      num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                      max_position_embeddings=8192, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    with torch.device(gpu):
+        model = LlamaForCausalLM(cfg)
+    for p in model.parameters():
+        p.data.normal_(0.0, 0.06)
+    model = model.half().eval()
+    install_llama_phasekv_attention(model)
+    g = torch.Generator().manual_seed(3)
+    prompt = torch.randint(0, 2000, (1, 200), generator=g).to(gpu)
+    _, cache = phasekv_prefill(model, prompt, prompt_bits=8, cold_bits=8)
+    dense = DynamicCache(config=cfg)
+    tok = model(prompt, past_key_values=dense, use_cache=True).logits[:, -1].argmax(-1, keepdim=True)
+    for step in range(52):
+        mine = phasekv_step(model, tok, cache)
+        want = model(tok, past_key_values=dense, use_cache=True).logits[:, -1]
+        cos, rel = _close(mine, want)
+        assert cos > 0.999 and rel < 0.05, (step, cos, rel)
+        tok = want.argmax(-1, keepdim=True)
+    chunk = torch.randint(0, 2000, (1, 9), generator=g).to(gpu)
+    cos, rel = _close(phasekv_step(model, chunk, cache),
+                      model(chunk, past_key_values=dense, use_cache=True).logits[:, -1])
+    assert cos > 0.999 and rel < 0.05 and len(cache.layer_tiers(0).cold) == 1
