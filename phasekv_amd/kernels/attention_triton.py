@@ -207,6 +207,24 @@ def _remove_batch(pt: PackedTensor) -> PackedTensor:
                    orig_shape=tuple(pt.orig_shape[1:]), axis=pt.axis - 1)
 
 
+def _kivi_segment(segment, splits: int, split_len: int) -> _dec.Segment:
+    """The decode segment of a batch-1 ``PackedKVSegment``, built once per segment object
+    (packed segments do not change after they are made) and per launch override."""
+    hit = getattr(segment, "_pk_decode_segment", None)
+    if (hit is not None and hit[0] == (splits, split_len) and hit[1] is segment.key
+            and hit[2] is segment.value):
+        return hit[3]
+    key, value = _remove_batch(segment.key), _remove_batch(segment.value)
+    if key.axis != 1 or value.axis != 2:
+        raise ValueError("K must be packed along tokens and V along head_dim")
+    seg = _dec.packed_segment(key, value, batched=False, splits=splits, split_len=split_len)
+    try:
+        segment._pk_decode_segment = ((splits, split_len), segment.key, segment.value, seg)
+    except AttributeError:      # a caller's segment type without instance attributes
+        pass
+    return seg
+
+
 def phasekv_problem(q: torch.Tensor, tiers, num_attention_heads: int, batched: bool = False,
                     prompt_lens: torch.Tensor | None = None, num_splits: int | None = None,
                     block_n: int | None = None, num_warps: int | None = None) -> _dec.Problem:
@@ -218,14 +236,12 @@ def phasekv_problem(q: torch.Tensor, tiers, num_attention_heads: int, batched: b
             segs.append(_dec.packed_segment(segment.key, segment.value, batched=True,
                                             seq_lens=lens))
             continue
-        key, value = _remove_batch(segment.key), _remove_batch(segment.value)
-        if key.axis != 1 or value.axis != 2:
-            raise ValueError("K must be packed along tokens and V along head_dim")
-        hkv, seq_len, head_dim = key.orig_shape
-        splits, split_len = _override_plan(seq_len, num_attention_heads, head_dim, q.device,
+        shape = tuple(segment.key.orig_shape)
+        if len(shape) != 4:
+            raise ValueError("packed K/V must be [1, Hkv, S, hd]")
+        splits, split_len = _override_plan(shape[2], num_attention_heads, shape[3], q.device,
                                            num_splits, block_n, num_warps)
-        segs.append(_dec.packed_segment(key, value, batched=False, splits=splits,
-                                        split_len=split_len))
+        segs.append(_kivi_segment(segment, splits, split_len))
     if tiers.hot_len:
         hot_k, hot_v = tiers.hot_views()
         segs.append(_dec.fp16_segment(hot_k if batched else hot_k[0],
