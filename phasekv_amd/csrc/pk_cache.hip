@@ -272,65 +272,83 @@ cool_pack_staged_kernel(uint16_t* hk, uint16_t* hv, HotView hot, int Hkv, int hd
   int* kidx = reinterpret_cast<int*>(st.tail);                      // [keep]: token of kept row
   pk::GroupStats* kst = reinterpret_cast<pk::GroupStats*>(kidx + keep + (keep & 1));  // [ngk][hd]
   pk::GroupStats* vst = kst + po.ngk * hd;                            // [keep][ngv]
+  // the kept rows, dense and in output order: kk[j][c], vv[j][c]
+  const int pr = hd / 8;
+  uint4* kkq = reinterpret_cast<uint4*>(((reinterpret_cast<uintptr_t>(vst + keep * po.ngv)) + 15) &
+                                        ~uintptr_t(15));
+  uint4* vvq = kkq + keep * pr;
   for (int t = tid; t < aged; t += kCoolThreads)
     if (st.pos[t] >= 0) kidx[st.pos[t]] = t;
   __syncthreads();
-  const uint16_t* skh = reinterpret_cast<const uint16_t*>(st.sk);
-  const uint16_t* svh = reinterpret_cast<const uint16_t*>(st.sv);
-  // group statistics and the fp16 scale / min
-  for (int i = tid; i < po.ngk * hd; i += kCoolThreads) {
-    const int g = i / hd, c = i - g * hd;
-    const int j0 = g * po.gsk, j1 = min(j0 + po.gsk, keep);
-    float mn = pk_h2f(skh[kidx[j0] * hd + c]), mx = mn;
-    for (int j = j0 + 1; j < j1; ++j) {
-      const float x = pk_h2f(skh[kidx[j] * hd + c]);
-      mn = pk::nan_min(mn, x);
-      mx = pk::nan_max(mx, x);
-    }
-    const pk::GroupStats s = pk::group_stats_from(mn, mx, po.bits);
-    kst[i] = s;
-    po.ks[(bh * po.ngk + g) * hd + c] = pk_f2h(s.scale);
-    po.km[(bh * po.ngk + g) * hd + c] = pk_f2h(s.mn);
-  }
-  for (int i = tid; i < keep * po.ngv; i += kCoolThreads) {
-    const int j = i / po.ngv, g = i - j * po.ngv;
-    const uint16_t* row = svh + kidx[j] * hd;
-    const int c0 = g * po.gsv, c1 = min(c0 + po.gsv, hd);
-    float mn = pk_h2f(row[c0]), mx = mn;
-    for (int c = c0 + 1; c < c1; ++c) {
-      const float x = pk_h2f(row[c]);
-      mn = pk::nan_min(mn, x);
-      mx = pk::nan_max(mx, x);
-    }
-    const pk::GroupStats s = pk::group_stats_from(mn, mx, po.bits);
-    vst[i] = s;
-    po.vs[(bh * keep + j) * po.ngv + g] = pk_f2h(s.scale);
-    po.vm[(bh * keep + j) * po.ngv + g] = pk_f2h(s.mn);
+  for (int i = tid; i < keep * pr; i += kCoolThreads) {
+    const int j = i / pr, c = i - j * pr;
+    kkq[i] = st.sk[kidx[j] * pr + c];
+    vvq[i] = st.sv[kidx[j] * pr + c];
   }
   __syncthreads();
-  // code bytes, LSB first, zero codes past the end of the axis
-  const int vpb = 8 / po.bits;
-  for (int i = tid; i < po.nbk * hd; i += kCoolThreads) {
-    const int byte = i / hd, c = i - byte * hd;
-    uint32_t x = 0;
-    for (int k = 0; k < vpb; ++k) {
-      const int j = byte * vpb + k;
-      if (j < keep)
-        x |= pk::quant_code(pk_h2f(skh[kidx[j] * hd + c]), kst[(j / po.gsk) * hd + c], po.bits)
-             << (k * po.bits);
+  const uint16_t* kk = reinterpret_cast<const uint16_t*>(kkq);
+  const uint16_t* vv = reinterpret_cast<const uint16_t*>(vvq);
+  // group statistics and the fp16 scale / min: K items (g, c) on the first threads,
+  // V items (j, g) after them, in one pass
+  const int nks = po.ngk * hd, nvs = keep * po.ngv;
+  for (int i = tid; i < nks + nvs; i += kCoolThreads) {
+    float mn, mx;
+    if (i < nks) {
+      const int g = i / hd, c = i - g * hd;
+      const int j0 = g * po.gsk, j1 = min(j0 + po.gsk, keep);
+      mn = mx = pk_h2f(kk[j0 * hd + c]);
+      for (int j = j0 + 1; j < j1; ++j) {
+        const float x = pk_h2f(kk[j * hd + c]);
+        mn = pk::nan_min(mn, x);
+        mx = pk::nan_max(mx, x);
+      }
+      const pk::GroupStats s = pk::group_stats_from(mn, mx, po.bits);
+      kst[i] = s;
+      po.ks[(bh * po.ngk + g) * hd + c] = pk_f2h(s.scale);
+      po.km[(bh * po.ngk + g) * hd + c] = pk_f2h(s.mn);
+    } else {
+      const int iv = i - nks;
+      const int j = iv / po.ngv, g = iv - j * po.ngv;
+      const uint16_t* row = vv + j * hd;
+      const int c0 = g * po.gsv, c1 = min(c0 + po.gsv, hd);
+      mn = mx = pk_h2f(row[c0]);
+      for (int c = c0 + 1; c < c1; ++c) {
+        const float x = pk_h2f(row[c]);
+        mn = pk::nan_min(mn, x);
+        mx = pk::nan_max(mx, x);
+      }
+      const pk::GroupStats s = pk::group_stats_from(mn, mx, po.bits);
+      vst[iv] = s;
+      po.vs[(bh * keep + j) * po.ngv + g] = pk_f2h(s.scale);
+      po.vm[(bh * keep + j) * po.ngv + g] = pk_f2h(s.mn);
     }
-    po.kp[(bh * po.nbk + byte) * hd + c] = static_cast<uint8_t>(x);
   }
-  for (int i = tid; i < keep * po.nbv; i += kCoolThreads) {
-    const int j = i / po.nbv, byte = i - j * po.nbv;
-    const uint16_t* row = svh + kidx[j] * hd;
+  __syncthreads();
+  // code bytes, LSB first, zero codes past the end of the axis: K bytes, then V bytes
+  const int vpb = 8 / po.bits;
+  const int nkb = po.nbk * hd, nvb = keep * po.nbv;
+  for (int i = tid; i < nkb + nvb; i += kCoolThreads) {
     uint32_t x = 0;
-    for (int k = 0; k < vpb; ++k) {
-      const int c = byte * vpb + k;
-      if (c < hd)
-        x |= pk::quant_code(pk_h2f(row[c]), vst[j * po.ngv + c / po.gsv], po.bits) << (k * po.bits);
+    if (i < nkb) {
+      const int byte = i / hd, c = i - byte * hd;
+      for (int k = 0; k < vpb; ++k) {
+        const int j = byte * vpb + k;
+        if (j < keep)
+          x |= pk::quant_code(pk_h2f(kk[j * hd + c]), kst[(j / po.gsk) * hd + c], po.bits)
+               << (k * po.bits);
+      }
+      po.kp[(bh * po.nbk + byte) * hd + c] = static_cast<uint8_t>(x);
+    } else {
+      const int iv = i - nkb;
+      const int j = iv / po.nbv, byte = iv - j * po.nbv;
+      const uint16_t* row = vv + j * hd;
+      for (int k = 0; k < vpb; ++k) {
+        const int c = byte * vpb + k;
+        if (c < hd)
+          x |= pk::quant_code(pk_h2f(row[c]), vst[j * po.ngv + c / po.gsv], po.bits) << (k * po.bits);
+      }
+      po.vp[(bh * keep + j) * po.nbv + byte] = static_cast<uint8_t>(x);
     }
-    po.vp[(bh * keep + j) * po.nbv + byte] = static_cast<uint8_t>(x);
   }
   if (oidx)
     for (int j = tid; j < keep; j += kCoolThreads) oidx[bh * keep + j] = kidx[j];
@@ -342,7 +360,9 @@ static size_t staged_lds(int64_t hot_len, int hd, int64_t aged, int64_t keep, bo
                          int64_t ngk, int64_t ngv) {
   if (hd % 8) return 0;
   size_t bytes = (size_t)4 * hot_len * hd + (size_t)8 * aged;
-  if (pack) bytes += (size_t)4 * (keep + (keep & 1)) + sizeof(pk::GroupStats) * (ngk * hd + keep * ngv);
+  if (pack)
+    bytes += (size_t)4 * (keep + (keep & 1)) + sizeof(pk::GroupStats) * (ngk * hd + keep * ngv) +
+             15 + (size_t)4 * keep * hd;   // kept rows, dense, 16-byte aligned
   return bytes <= kCoolStagedLds ? bytes : 0;
 }
 
