@@ -228,6 +228,8 @@ def _bench_prompt_chunk(cfg, device, T, steps, warmup, stream):
     q = torch.randn(T, cfg.hq, cfg.hd, generator=gen).to(torch.float16).to(device)
     one = _time_graph([lambda: fused_phasekv_prompt_chunk_attention(q, tiers, cfg.hq)], steps,
                       warmup, stream)
+    by = {m: _time_graph([lambda m=m: fused_phasekv_prompt_chunk_attention(q, tiers, cfg.hq, m)],
+                         steps, warmup, stream) for m in ("heads", "batch")}
     views = [dataclasses.replace(tiers, hot_len=cfg.hot + t + 1) for t in range(T)]
 
     def loop():
@@ -238,7 +240,8 @@ def _bench_prompt_chunk(cfg, device, T, steps, warmup, stream):
     del wl, tiers, views
     torch.cuda.empty_cache()
     return {"config": f"{cfg.name}-prompt-chunk", "chunk_tokens": T, "chunk_us": one * 1e6,
-            "us_per_chunk_token": one * 1e6 / T, "per_token_loop_us": lsec * 1e6,
+            "us_per_chunk_token": one * 1e6 / T, "heads_us": by["heads"] * 1e6,
+            "batch_us": by["batch"] * 1e6, "per_token_loop_us": lsec * 1e6,
             "speedup_vs_loop": lsec / one}
 
 

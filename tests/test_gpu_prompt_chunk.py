@@ -63,6 +63,9 @@ def test_chunk_attention_matches_the_per_token_loop(gpu, hq, hkv, hd, T, decode_
     start = tiers.hot_len - T
     q = torch.randn(T, hq, hd, generator=g).to(torch.float16)
     out = fused_phasekv_prompt_chunk_attention(q.to(gpu), tiers, hq).float().cpu().numpy()
+    for method in ("heads", "batch"):
+        other = fused_phasekv_prompt_chunk_attention(q.to(gpu), tiers, hq, method=method)
+        np.testing.assert_allclose(other.float().cpu().numpy(), out, atol=1e-3, rtol=1e-2)
     loop = np.stack([fused_phasekv_decode(q[t].to(gpu), dataclasses.replace(tiers, hot_len=start + t + 1),
                                           hq).float().cpu().numpy() for t in range(T)])
     want = np.stack([ao.segments_attention(q[t].numpy(), _segments(tiers, start + t + 1), hq)
