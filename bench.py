@@ -96,9 +96,20 @@ def _bench_config(cfg, device, steps, warmup, stream, with_dense=True):
     # the dominant kernel alone: the same steps without the combine launch
     ksec = _time_graph([lambda pr=pr: dec.launch_partials(pr) for pr in probs], steps, warmup,
                        stream)
+    # one eager call, host call to completion (launch overheads included), median of 50
+    lat = []
+    with torch.cuda.stream(stream):
+        for i in range(60):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fns[i % len(fns)]()
+            torch.cuda.synchronize()
+            lat.append(time.perf_counter() - t0)
+    single = sorted(lat[10:])[len(lat[10:]) // 2]
     res = {"config": cfg.name, "tokens": cfg.tokens, "bytes": nbytes, "copies": copies,
            "us_per_step": sec * 1e6, "gbs": nbytes / sec / 1e9,
-           "partials_us": ksec * 1e6, "partials_gbs": nbytes / ksec / 1e9}
+           "partials_us": ksec * 1e6, "partials_gbs": nbytes / ksec / 1e9,
+           "single_call_us": single * 1e6}
     res["frac"] = res["gbs"] / HBM_PEAK_GBS
     del tiers, fns, probs
     if with_dense:
@@ -509,6 +520,7 @@ def main() -> int:
                      "launch_us": round(main_res["partials_us"], 3)},
         "cpu_baseline": cpu,
         "us_per_step": round(main_res["us_per_step"], 3),
+        "single_call_us": round(main_res["single_call_us"], 3),
         "fp16_dense_us": round(main_res.get("fp16_dense_us", float("nan")), 3),
         "speedup_vs_fp16": round(main_res.get("speedup_vs_fp16", float("nan")), 4),
         "rotating_copies": main_res["copies"],

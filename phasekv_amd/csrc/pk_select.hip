@@ -37,7 +37,7 @@ __device__ __forceinline__ float load_attn(const AttnView& a, int64_t off) {
 // the last w query rows r (in order) of attention[b, kv * G + g, q_len - w + r, j],
 // all in float32.  A workgroup takes 64 * KPL key positions of one (b, kv): wave s
 // sums the rows of query heads s, s + 4, ... (KPL neighbouring keys per lane in one
-// load, 8 rows of loads in flight, added in row order), and wave 0 adds the heads'
+// load, 16 rows of loads in flight, added in row order), and wave 0 adds the heads'
 // sums in head order.
 constexpr int kMaxGroup = 32;
 
@@ -72,12 +72,12 @@ votes_kernel(AttnView a, int Hkv, int G, int64_t q_len, int64_t kv_len, int w,
 #pragma unroll
     for (int i = 0; i < KPL; ++i) sum[i] = 0.f;
     int r = 0;
-    for (; r + 8 <= w; r += 8) {
-      float x[8][KPL];
+    for (; r + 16 <= w; r += 16) {
+      float x[16][KPL];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) load_keys<KPL, void>(a, base + (r + u) * a.sq, x[u]);
+      for (int u = 0; u < 16; ++u) load_keys<KPL, void>(a, base + (r + u) * a.sq, x[u]);
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < 16; ++u)
 #pragma unroll
         for (int i = 0; i < KPL; ++i) sum[i] = __fadd_rn(sum[i], x[u][i]);
     }
