@@ -34,12 +34,16 @@ Pinning status (what checks each function independently of its own formula):
   calls the reference makes) on tie-free inputs; norms within 1 ulp-scale of a
   float64 norm; ties and NaN by brute force over explicit rankings; the cooled
   segment equals ``quantize_pack`` of the kept rows and the shifted window equals
-  slicing; ``keep_count`` against Python's round on half-way cases.
+  slicing; ``keep_count`` against Python's round on half-way cases.  Parity unpinned:
+  which of several tokens with exactly equal V norms is kept (``torch.topk`` does not
+  fix it; here the earlier token).
 * select_oracle (votes, pooling, kept positions) — votes, pooling and the kept set
   equal torch's own ``float().sum``, ``F.max_pool1d`` / ``F.avg_pool1d`` and
   ``topk().indices`` (the calls the reference makes) on tie-free inputs; the plan
   against hand-worked budgets; max pooling exact against a brute-force window max;
-  ties and NaN by brute force.
+  ties and NaN by brute force.  Parity unpinned: which of several candidates with
+  exactly equal pooled scores is kept (``torch.topk`` does not fix it; here the earlier
+  position), and the votes' float32 summation order against torch's reduction order.
 * plan_kivi_decode — known-answer tests from the reference's
   ``tests/test_phasekv_launch_config.py:10-47`` and the published plan table
   (``docs/idea/PhaseKV-技术原理与系统设计.md:495-502``).
