@@ -208,8 +208,10 @@ class Problem:
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
 
 
-def cached_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    stream = _lib.stream_ptr(device)
+def cached_workspace(device: torch.device, nbytes: int,
+                     stream: Optional[int] = None) -> torch.Tensor:
+    if stream is None:
+        stream = _lib.stream_ptr(device)
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
@@ -222,13 +224,12 @@ def cached_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def fused_decode(problem: Problem) -> torch.Tensor:
     """Normalized attention output [B, Hq, hd] fp16: one partial launch (per 8 segments) + combine."""
     nbytes, _ = problem.workspace_size()
-    ws = cached_workspace(problem.device, nbytes)
+    stream = _lib.stream_ptr(problem.device)
+    ws = cached_workspace(problem.device, nbytes, stream)
     out = torch.empty(problem.batch, problem.hq, problem.hd, dtype=torch.float16,
                       device=problem.device)
-    lib = _lib.load()
-    _lib.check(lib.pk_fused_decode(ctypes.byref(problem.c), ws.data_ptr(), ws.numel(),
-                                   out.data_ptr(), _lib.stream_ptr(problem.device)),
-               "fused_decode")
+    _lib.check(_lib.load().pk_fused_decode(ctypes.byref(problem.c), ws.data_ptr(), ws.numel(),
+                                           out.data_ptr(), stream), "fused_decode")
     return out
 
 

@@ -225,6 +225,51 @@ def _kivi_segment(segment, splits: int, split_len: int) -> _dec.Segment:
     return seg
 
 
+def _reused_problem(q: torch.Tensor, tiers, num_attention_heads: int) -> _dec.Problem:
+    """The batch-1 decode problem of ``tiers``, kept on the tiers object across calls.
+
+    Between cooling events a layer's packed segments and its hot buffer stay the same
+    objects; a decode step changes only q and the hot window's length.  The problem
+    (descriptors, C arrays, device checks) is rebuilt when the segment list, the hot
+    buffer or the head count changes; otherwise the call writes q's pointer and
+    strides and the hot segment's length into the kept C structure.  The launch copies
+    the descriptors into its kernel arguments, so the next call may overwrite them.
+    """
+    packed = [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]
+    hot_len = tiers.hot_len
+    hot = (tiers.hot_k, tiers.hot_v) if hot_len else None
+    kept = getattr(tiers, "_pk_problem", None)
+    if kept is not None:
+        k_packed, k_hot, k_hq, problem = kept
+        if (k_hq == num_attention_heads and len(k_packed) == len(packed)
+                and all(a is b for a, b in zip(k_packed, packed))
+                and (k_hot is None) == (hot is None)
+                and (hot is None or (k_hot[0] is hot[0] and k_hot[1] is hot[1]))
+                and q.dtype == torch.float16 and q.dim() == 2 and q.is_cuda
+                and q.get_device() == problem.device.index
+                and q.shape[0] == problem.hq and q.shape[1] == problem.hd):
+            if q.stride(-1) != 1:
+                q = q.contiguous()
+            q3 = q.unsqueeze(0)
+            problem.q = q3
+            problem.c.q = q3.data_ptr()
+            problem.c.q_bstride, problem.c.q_hstride = q3.stride(0), q3.stride(1)
+            if hot is not None:
+                problem._arr[len(packed)].length = hot_len
+                problem.segments[-1].length = hot_len
+            return problem
+    problem = phasekv_problem(q, tiers, num_attention_heads)
+    if hot is not None:
+        d = problem.segments[-1].desc
+        if d.k_data != hot[0].data_ptr() or d.v_data != hot[1].data_ptr():
+            return problem      # the hot window was copied, not read in place: no reuse
+    try:
+        tiers._pk_problem = (packed, hot, num_attention_heads, problem)
+    except AttributeError:      # a caller's tiers type without instance attributes
+        pass
+    return problem
+
+
 def phasekv_problem(q: torch.Tensor, tiers, num_attention_heads: int, batched: bool = False,
                     prompt_lens: torch.Tensor | None = None, num_splits: int | None = None,
                     block_n: int | None = None, num_warps: int | None = None) -> _dec.Problem:
@@ -258,8 +303,11 @@ def fused_phasekv_decode(q: torch.Tensor, tiers, num_attention_heads: int,
     ``prompt_extensions``, ``cold``, ``hot_len`` and ``hot_views()``).  q ``[Hq, hd]``
     fp16 -> ``[Hq, hd]`` fp16 (``attention_triton.py:643-669``).
     """
-    problem = phasekv_problem(q, tiers, num_attention_heads, num_splits=num_splits,
-                              block_n=block_n, num_warps=num_warps)
+    if num_splits is None and block_n is None and num_warps is None:
+        problem = _reused_problem(q, tiers, num_attention_heads)
+    else:
+        problem = phasekv_problem(q, tiers, num_attention_heads, num_splits=num_splits,
+                                  block_n=block_n, num_warps=num_warps)
     return _dec.fused_decode(problem)[0]
 
 

@@ -4,7 +4,7 @@ Mirrors the duck-typed contract of ``PackedKVSegment`` / ``LayerTiers``
 (``src/phasekv/phasekv_cache.py:30-79``) and the cache's K/V packing convention
 ``_pack_kv`` (``src/phasekv/phasekv_cache.py:101-107``): K is quantized per
 channel along tokens (``axis=-2``), V per token along head_dim (``axis=-1``).
-The cache's lifecycle (cooling, prompt chunks) is not part of this package.
+The cache's lifecycle (append, cooling, prompt chunks) is ``phasekv_amd.cache``.
 """
 from __future__ import annotations
 

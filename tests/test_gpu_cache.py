@@ -309,3 +309,64 @@ def test_reorder_cache_keeps_storage_and_rows(gpu):
     assert torch.equal(after, before[idx])
     with pytest.raises(ValueError, match="beam_idx"):
         cache.reorder_cache(torch.tensor([3], dtype=torch.long, device=gpu))
+
+
+def test_reused_decode_problem_matches_a_fresh_one(gpu):
+    """The batch-1 decode keeps each layer's problem across steps and only rewrites q and
+    the hot length: every step's output equals, bit for bit, the output of a problem built
+    from scratch, through a cooling event (new cold segment), a prompt chunk (new
+    extension, new hot buffer), a strided q and a new q tensor every step; the oracle
+    checks every tenth step."""
+    from phasekv_amd import decode as dec
+    from phasekv_amd.cache import PhaseKVCache
+    from phasekv_amd.kernels.attention_triton import fused_phasekv_decode, phasekv_problem
+    g = torch.Generator().manual_seed(11)
+    B, H, hq, hd, S = 1, 2, 8, 128, 96
+    keys = [torch.randn(B, H, S, hd, generator=g).to(torch.float16)]
+    values = [torch.randn(B, H, S, hd, generator=g).to(torch.float16)]
+    cache = PhaseKVCache.from_dense_prefill(
+        _Dense([k.to(gpu) for k in keys], [v.to(gpu) for v in values]), prompt_len=S,
+        prompt_bits=2, cold_bits=4, group_size=32, recent_window=32, lazy_g=16,
+        decode_keep_ratio=0.5)
+    rebuilt = []
+
+    def step_and_check(step):
+        tiers = cache.layer_tiers(0)
+        if step % 7 == 3:
+            q = torch.randn(hd, hq, generator=g).to(torch.float16).to(gpu).t()   # stride(-1) != 1
+        else:
+            q = torch.randn(hq, hd, generator=g).to(torch.float16).to(gpu)
+        kept = getattr(tiers, "_pk_problem", None)
+        got = fused_phasekv_decode(q, tiers, hq)
+        rebuilt.append(kept is None or tiers._pk_problem is not kept)
+        fresh = dec.fused_decode(phasekv_problem(q, tiers, hq))[0]
+        assert torch.equal(got, fresh), f"step {step}"
+        if step % 10 == 0:
+            segs = [(s.key, s.value) for s in [tiers.prompt, *tiers.prompt_extensions,
+                                                *tiers.cold]]
+            deq = [(po.dequantize_float(_np_pt(k))[0], po.dequantize_float(_np_pt(v))[0])
+                   for k, v in segs]
+            hk, hv = tiers.hot_views()
+            deq.append((hk[0].cpu().numpy(), hv[0].cpu().numpy()))
+            want = ao.segments_attention(q.cpu().numpy(), deq, hq)
+            np.testing.assert_allclose(got.float().cpu().numpy(), want, atol=2e-3, rtol=1e-2)
+
+    for step in range(60):
+        nk = torch.randn(B, H, 1, hd, generator=g).to(torch.float16).to(gpu)
+        nv = torch.randn(B, H, 1, hd, generator=g).to(torch.float16).to(gpu)
+        cache.append_hot(0, nk, nv)
+        step_and_check(step)
+        cache.finish_decode_step()
+    assert len(cache.layer_tiers(0).cold) == 1
+    cache.begin_prompt_chunk(5)
+    for i in range(5):
+        cache.append_prompt_token(0, torch.randn(B, H, 1, hd, generator=g).to(torch.float16).to(gpu),
+                                  torch.randn(B, H, 1, hd, generator=g).to(torch.float16).to(gpu))
+    cache.finish_prompt_chunk()
+    for step in range(60, 64):
+        cache.append_hot(0, torch.randn(B, H, 1, hd, generator=g).to(torch.float16).to(gpu),
+                         torch.randn(B, H, 1, hd, generator=g).to(torch.float16).to(gpu))
+        step_and_check(step)
+        cache.finish_decode_step()
+    # built at the first step, after the cooling at step 47 and after the prompt chunk only
+    assert [i for i, r in enumerate(rebuilt) if r] == [0, 48, 60]
