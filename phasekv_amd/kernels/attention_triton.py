@@ -228,14 +228,16 @@ def _kivi_segment(segment, splits: int, split_len: int) -> _dec.Segment:
 def _reused_problem(q: torch.Tensor, tiers, num_attention_heads: int) -> _dec.Problem:
     """The batch-1 decode problem of ``tiers``, kept on the tiers object across calls.
 
-    Between cooling events a layer's packed segments and its hot buffer stay the same
-    objects; a decode step changes only q and the hot window's length.  The problem
-    (descriptors, C arrays, device checks) is rebuilt when the segment list, the hot
-    buffer or the head count changes; otherwise the call writes q's pointer and
-    strides and the hot segment's length into the kept C structure.  The launch copies
-    the descriptors into its kernel arguments, so the next call may overwrite them.
+    Between cooling events a layer's packed K/V (``PackedTensor`` objects) and its hot
+    buffer stay the same objects; a decode step changes only q and the hot window's
+    length.  The problem (descriptors, C arrays, device checks) is rebuilt when the
+    packed K/V list, the hot buffer or the head count changes; otherwise the call writes
+    q's pointer and strides and the hot segment's length into the kept C structure.  The
+    launch copies the descriptors into its kernel arguments, so the next call may
+    overwrite them.
     """
-    packed = [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]
+    segments = [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]
+    packed = [t for s in segments for t in (s.key, s.value)]
     hot_len = tiers.hot_len
     hot = (tiers.hot_k, tiers.hot_v) if hot_len else None
     kept = getattr(tiers, "_pk_problem", None)
@@ -255,7 +257,7 @@ def _reused_problem(q: torch.Tensor, tiers, num_attention_heads: int) -> _dec.Pr
             problem.c.q = q3.data_ptr()
             problem.c.q_bstride, problem.c.q_hstride = q3.stride(0), q3.stride(1)
             if hot is not None:
-                problem._arr[len(packed)].length = hot_len
+                problem._arr[len(segments)].length = hot_len
                 problem.segments[-1].length = hot_len
             return problem
     problem = phasekv_problem(q, tiers, num_attention_heads)
