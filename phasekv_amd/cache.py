@@ -9,6 +9,8 @@ decode loop:
   ``keep_indices`` and packing)
 * ``append_hot``           ``phasekv_cache.py:291-301`` and ``_append_token``
   ``:405-422`` (one HIP launch writes K and V)
+* ``rope_append_hot``      the adapters' rotary embedding plus ``append_hot`` of one
+  decode token (``qwen2_attention.py:89-92, 77``) in one HIP launch
 * ``finish_decode_step``   ``phasekv_cache.py:302-320``
 * ``_cool_aged_tokens``    ``phasekv_cache.py:322-340``: one HIP launch ranks the
   aged tokens by value norm, gathers and packs the kept ones into the new cold
@@ -321,6 +323,72 @@ class PhaseKVCache:
                                "finish_decode_step() after the forward pass")
         self._append_token(layer_idx, layer, key, value)
         self._pending_layers.add(layer_idx)
+
+    @torch.no_grad()
+    def rope_append_hot(self, layer_idx: int, query: torch.Tensor, key: torch.Tensor,
+                        value: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                        num_attention_heads: int) -> torch.Tensor:
+        """``apply_rotary_pos_emb`` (rotate_half form) and ``append_hot`` of one decode
+        token in one launch; returns the rotated query ``[B, Hq, hd]`` fp16.
+
+        ``query`` / ``key`` / ``value`` are the fp16 projections ``[B, 1, H*hd]`` (head_dim
+        contiguous), ``cos`` / ``sin`` fp16 ``[B or 1, 1, hd]``.  The rotated K and the V
+        go into the window as ``append_hot`` writes them, bit-identical to rotating the
+        fp16 tensors with ``x * cos + rotate_half(x) * sin`` first
+        (``qwen2_attention.py:89-92, 77``).
+        """
+        if self._prompt_chunk_len:
+            raise RuntimeError("a prompt chunk is open: append with append_prompt_token() and "
+                               "close it with finish_prompt_chunk()")
+        layer = self.layer_tiers(layer_idx)
+        if layer_idx in self._pending_layers:
+            raise RuntimeError(f"layer {layer_idx} already appended in this decode step; call "
+                               "finish_decode_step() after the forward pass")
+        hk, hv = layer.hot_k, layer.hot_v
+        B, hkv, cap, hd = hk.shape
+        hq = int(num_attention_heads)
+        tensors = (query, key, value, cos, sin)
+        if not all(isinstance(t, torch.Tensor) for t in tensors):
+            raise TypeError(f"layer {layer_idx} query / key / value / cos / sin must be tensors")
+        if any(t.dtype != torch.float16 for t in tensors):
+            raise ValueError(f"layer {layer_idx} query / key / value / cos / sin must be float16")
+        if hq <= 0 or hq % hkv:
+            raise ValueError(f"num_attention_heads {hq} must be a positive multiple of {hkv}")
+        if (tuple(query.shape) != (B, 1, hq * hd) or tuple(key.shape) != (B, 1, hkv * hd)
+                or key.shape != value.shape):
+            raise ValueError(f"layer {layer_idx} projections must be [B, 1, H*hd] = "
+                             f"{(B, 1, hq * hd)} / {(B, 1, hkv * hd)}, got {tuple(query.shape)} / "
+                             f"{tuple(key.shape)} / {tuple(value.shape)}")
+        if cos.shape != sin.shape or cos.dim() != 3 or cos.shape[0] not in (1, B) \
+                or tuple(cos.shape[1:]) != (1, hd):
+            raise ValueError(f"cos / sin must be [B or 1, 1, {hd}], got {tuple(cos.shape)} / "
+                             f"{tuple(sin.shape)}")
+        dev = hk.device
+        if any(t.device != dev for t in tensors):
+            raise ValueError(f"layer {layer_idx} tensors must be on the hot window's device {dev}")
+        if layer.hot_len >= cap:
+            raise RuntimeError(f"layer {layer_idx} hot window is full: hot_len={layer.hot_len}, "
+                               f"capacity={cap}")
+        if hk.stride() != hv.stride() or hk.stride(-1) != 1:
+            raise ValueError("hot_k and hot_v must share strides with a contiguous head_dim")
+        if query.stride(-1) != 1:
+            query = query.contiguous()
+        if key.stride(-1) != 1 or value.stride(-1) != 1 or key.stride(0) != value.stride(0):
+            key, value = key.contiguous(), value.contiguous()
+        if cos.stride(-1) != 1 or sin.stride(-1) != 1 or cos.stride(0) != sin.stride(0):
+            cos, sin = cos.contiguous(), sin.contiguous()
+        q_out = torch.empty(B, hq, hd, dtype=torch.float16, device=dev)
+        cs_bstride = cos.stride(0) if cos.shape[0] == B and B > 1 else 0
+        q_bstride = query.stride(0) if B > 1 else hq * hd     # unused for one row
+        kv_bstride = key.stride(0) if B > 1 else hkv * hd
+        _lib.check(_lib.load().pk_rope_append_hot(
+            query.data_ptr(), q_bstride, key.data_ptr(), value.data_ptr(), kv_bstride,
+            cos.data_ptr(), sin.data_ptr(), cs_bstride, q_out.data_ptr(), hk.data_ptr(),
+            hv.data_ptr(), hk.stride(0), hk.stride(1), hk.stride(2), B, hq, hkv, hd,
+            layer.hot_len, cap, _lib.stream_ptr(dev)), "rope_append_hot")
+        layer.hot_len += 1
+        self._pending_layers.add(layer_idx)
+        return q_out
 
     def _append_token(self, layer_idx: int, layer: LayerTiers, key: torch.Tensor,
                       value: torch.Tensor) -> None:

@@ -43,6 +43,55 @@ append_hot_kernel(const uint16_t* __restrict__ ks, const uint16_t* __restrict__ 
   }
 }
 
+// One decode token's rotary embedding, fused with the window append: thread
+// (row, d) with d < hd/2 rotates the pair (d, d + hd/2) of one q head or one
+// kv head.  The arithmetic is the fp16 sequence of rotate_half RoPE,
+// x * cos + rotate_half(x) * sin, each product and the sum computed in float
+// and rounded to fp16 (so the result equals that expression on fp16 tensors).
+// q heads go to q_out [B, Hq, hd]; k heads are rotated into the window at
+// `position`, v heads are copied there.
+__device__ __forceinline__ uint16_t rope_half(float x, float c, float r, float sn) {
+  const float a = pk_h2f(pk_f2h(x * c));
+  const float b = pk_h2f(pk_f2h(r * sn));
+  return pk_f2h(a + b);
+}
+
+__global__ void __launch_bounds__(256)
+rope_append_kernel(const uint16_t* __restrict__ q, int64_t qsb, const uint16_t* __restrict__ k,
+                   const uint16_t* __restrict__ v, int64_t kvsb, const uint16_t* __restrict__ cs,
+                   const uint16_t* __restrict__ sn, int64_t csb, uint16_t* __restrict__ q_out,
+                   uint16_t* hk, uint16_t* hv, HotView hot, int Hq, int Hkv, int hd,
+                   int64_t position, int64_t total) {
+  const int half = hd / 2;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / half;
+    const int d = (int)(i - row * half);
+    const int64_t b = row / (Hq + Hkv);
+    const int h = (int)(row - b * (Hq + Hkv));
+    const uint16_t* cr = cs + b * csb;
+    const uint16_t* sr = sn + b * csb;
+    const float c1 = pk_h2f(cr[d]), c2 = pk_h2f(cr[d + half]);
+    const float s1 = pk_h2f(sr[d]), s2 = pk_h2f(sr[d + half]);
+    if (h < Hq) {
+      const uint16_t* x = q + b * qsb + (int64_t)h * hd;
+      const float x1 = pk_h2f(x[d]), x2 = pk_h2f(x[d + half]);
+      uint16_t* o = q_out + (b * Hq + h) * (int64_t)hd;
+      o[d] = rope_half(x1, c1, -x2, s1);
+      o[d + half] = rope_half(x2, c2, x1, s2);
+    } else {
+      const int hk_ = h - Hq;
+      const int64_t src = b * kvsb + (int64_t)hk_ * hd;
+      const float x1 = pk_h2f(k[src + d]), x2 = pk_h2f(k[src + d + half]);
+      const int64_t dst = b * hot.bs + hk_ * hot.hs + position * hot.ts;
+      hk[dst + d] = rope_half(x1, c1, -x2, s1);
+      hk[dst + d + half] = rope_half(x2, c2, x1, s2);
+      hv[dst + d] = v[src + d];
+      hv[dst + d + half] = v[src + d + half];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // cooling: one workgroup per (b, kv head)
 // ---------------------------------------------------------------------------
@@ -403,6 +452,35 @@ extern "C" int pk_append_hot(const uint16_t* k_src, const uint16_t* v_src, int64
                      HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
                      position, total);
   return pk::check_launch("append_hot");
+}
+
+extern "C" int pk_rope_append_hot(const uint16_t* q, int64_t q_bstride, const uint16_t* k,
+                                  const uint16_t* v, int64_t kv_bstride, const uint16_t* cos,
+                                  const uint16_t* sin, int64_t cs_bstride, uint16_t* q_out,
+                                  uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride,
+                                  int64_t hot_hstride, int64_t hot_tstride, int batch,
+                                  int num_q_heads, int num_kv_heads, int head_dim,
+                                  int64_t position, int64_t capacity, void* stream) {
+  pk::clear_error();
+  if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
+                         hot_tstride))
+    return rc;
+  if (!q || !k || !v || !cos || !sin || !q_out) return pk::fail("null q / K / V / cos / sin / q_out");
+  if (num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return pk::fail("num_q_heads must be a positive multiple of num_kv_heads");
+  if (head_dim % 2) return pk::fail("head_dim must be even for the rotary embedding");
+  if (q_bstride < (int64_t)num_q_heads * head_dim || kv_bstride < (int64_t)num_kv_heads * head_dim ||
+      cs_bstride < 0)
+    return pk::fail("q / K / V batch strides must cover their heads; cos / sin stride >= 0");
+  if (position < 0 || position >= capacity) return pk::fail("hot window is full");
+  const int64_t total = (int64_t)batch * (num_q_heads + num_kv_heads) * (head_dim / 2);
+  const int grid = (int)std::min<int64_t>(pk::cdiv(total, 256), 4096);
+  hipLaunchKernelGGL(rope_append_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), q, q_bstride, k, v, kv_bstride, cos, sin,
+                     cs_bstride, q_out, hot_k, hot_v,
+                     HotView{hot_bstride, hot_hstride, hot_tstride}, num_q_heads, num_kv_heads,
+                     head_dim, position, total);
+  return pk::check_launch("rope_append_hot");
 }
 
 extern "C" int pk_cool_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride,

@@ -13,6 +13,8 @@ from .qwen2_attention import PhaseKVAttention, phasekv_prefill, phasekv_step  # 
 
 
 class PhaseKVLlamaAttention(PhaseKVAttention):
+    fused_rope = True
+
     @staticmethod
     def rope(q, k, cos, sin):
         from transformers.models.llama.modeling_llama import apply_rotary_pos_emb

@@ -30,7 +30,11 @@ class PhaseKVAttention(nn.Module):
     """Reuses the wrapped attention's projections; handles single-token decode and input
     chunks on a ``PhaseKVCache``.  The layer only writes K/V and attends; the caller
     calls ``finish_decode_step`` / ``finish_prompt_chunk`` after the model's forward.
-    Subclasses give the model family's RoPE."""
+    Subclasses give the model family's RoPE; ``fused_rope`` says it is the rotate_half
+    form, which an fp16 decode step applies in the window-append launch
+    (``PhaseKVCache.rope_append_hot``)."""
+
+    fused_rope = False
 
     def __init__(self, original: nn.Module):
         super().__init__()
@@ -67,11 +71,20 @@ class PhaseKVAttention(nn.Module):
         base = self.original
         cfg = base.config
         hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, base.head_dim
+        if position_embeddings is None:
+            raise ValueError("position_embeddings (RoPE cos, sin at the true positions) are needed")
+        if (self.fused_rope and not cache.prompt_chunk_len
+                and hidden_states.dtype == torch.float16
+                and position_embeddings[0].dtype == torch.float16):
+            # one launch: q and k rotated, k and v written into the window
+            q = cache.rope_append_hot(self.layer_idx, base.q_proj(hidden_states),
+                                      base.k_proj(hidden_states), base.v_proj(hidden_states),
+                                      *position_embeddings, hq)
+            out = fused_phasekv_decode(q[0], cache.layer_tiers(self.layer_idx), hq)
+            return base.o_proj(out.reshape(batch, q_len, hq * hd)), None
         q = base.q_proj(hidden_states).view(batch, q_len, hq, hd).transpose(1, 2)
         k = base.k_proj(hidden_states).view(batch, q_len, hkv, hd).transpose(1, 2)
         v = base.v_proj(hidden_states).view(batch, q_len, hkv, hd).transpose(1, 2)
-        if position_embeddings is None:
-            raise ValueError("position_embeddings (RoPE cos, sin at the true positions) are needed")
         cos, sin = position_embeddings
         q, k = self.rope(q, k, cos, sin)
         q, k, v = q.to(torch.float16), k.to(torch.float16), v.to(torch.float16)
@@ -89,6 +102,8 @@ class PhaseKVAttention(nn.Module):
 
 class PhaseKVQwen2Attention(PhaseKVAttention):
     """``PhaseKVQwen2Attention`` of ``qwen2_attention.py:19-109``."""
+
+    fused_rope = True
 
     @staticmethod
     def rope(q, k, cos, sin):

@@ -370,3 +370,66 @@ def test_reused_decode_problem_matches_a_fresh_one(gpu):
         cache.finish_decode_step()
     # built at the first step, after the cooling at step 47 and after the prompt chunk only
     assert [i for i, r in enumerate(rebuilt) if r] == [0, 48, 60]
+
+
+@pytest.mark.parametrize("B,hq,hkv,hd,cos_rows,positions", [
+    (1, 28, 4, 128, 1, (5, 4100, 32767)), (2, 8, 2, 64, 2, (0, 77)), (3, 12, 4, 128, 1, (1234,))])
+def test_rope_append_hot_matches_apply_rotary_pos_emb(gpu, B, hq, hkv, hd, cos_rows, positions):
+    """One launch equals transformers' ``apply_rotary_pos_emb`` on the fp16 tensors followed
+    by ``append_hot``: the rotated q and the window rows bit for bit, at short and long
+    positions, with one cos / sin row for every batch row or one per row."""
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+    from phasekv_amd.cache import PhaseKVCache
+    print(f"case B={B} hq={hq} hkv={hkv} hd={hd} cos_rows={cos_rows}", flush=True)
+    g = torch.Generator().manual_seed(B * 100 + hd)
+    S = 40
+    dense = _Dense([torch.randn(B, hkv, S, hd, generator=g).to(torch.float16).to(gpu)],
+                   [torch.randn(B, hkv, S, hd, generator=g).to(torch.float16).to(gpu)])
+    fused = PhaseKVCache.from_dense_prefill(dense, prompt_len=S, prompt_bits=4, cold_bits=4,
+                                            group_size=32, recent_window=32, lazy_g=16)
+    plain = PhaseKVCache.from_dense_prefill(dense, prompt_len=S, prompt_bits=4, cold_bits=4,
+                                            group_size=32, recent_window=32, lazy_g=16)
+    inv = 1.0 / (1e6 ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    for pos in positions:
+        p = torch.tensor([pos + r for r in range(cos_rows)], dtype=torch.float32)
+        freqs = p[:, None] * inv[None, :]
+        emb = torch.cat((freqs, freqs), dim=-1)
+        cos = emb.cos().to(torch.float16)[:, None, :].to(gpu)
+        sin = emb.sin().to(torch.float16)[:, None, :].to(gpu)
+        q = (torch.randn(B, 1, hq * hd, generator=g) * 4).to(torch.float16).to(gpu)
+        k = (torch.randn(B, 1, hkv * hd, generator=g) * 4).to(torch.float16).to(gpu)
+        v = torch.randn(B, 1, hkv * hd, generator=g).to(torch.float16).to(gpu)
+        got_q = fused.rope_append_hot(0, q, k, v, cos, sin, hq)
+        qh = q.view(B, 1, hq, hd).transpose(1, 2)
+        kh = k.view(B, 1, hkv, hd).transpose(1, 2)
+        want_q, want_k = apply_rotary_pos_emb(qh, kh, cos, sin)
+        plain.append_hot(0, want_k, v.view(B, 1, hkv, hd).transpose(1, 2))
+        assert torch.equal(got_q, want_q[:, :, 0, :]), f"q at position {pos}"
+        fk, fv = fused.layer_tiers(0).hot_views()
+        pk_, pv = plain.layer_tiers(0).hot_views()
+        assert torch.equal(fk, pk_) and torch.equal(fv, pv), f"window at position {pos}"
+        fused.finish_decode_step()
+        plain.finish_decode_step()
+
+
+def test_rope_append_hot_errors(gpu):
+    from phasekv_amd.cache import PhaseKVCache
+    g = torch.Generator().manual_seed(5)
+    dense = _Dense([torch.randn(1, 2, 32, 64, generator=g).to(torch.float16).to(gpu)],
+                   [torch.randn(1, 2, 32, 64, generator=g).to(torch.float16).to(gpu)])
+    cache = PhaseKVCache.from_dense_prefill(dense, prompt_len=32, prompt_bits=2, cold_bits=2,
+                                            group_size=32, recent_window=4, lazy_g=2)
+    f16 = dict(dtype=torch.float16, device=gpu)
+    q, k, v = torch.zeros(1, 1, 8 * 64, **f16), torch.zeros(1, 1, 128, **f16), torch.zeros(1, 1, 128, **f16)
+    cs = torch.ones(1, 1, 64, **f16)
+    with pytest.raises(ValueError):
+        cache.rope_append_hot(0, q, k, v, cs, cs, 6)               # q is not [1, 1, 6 * 64]
+    with pytest.raises(ValueError):
+        cache.rope_append_hot(0, q.float(), k, v, cs, cs, 8)       # dtype
+    with pytest.raises(ValueError):
+        cache.rope_append_hot(0, q, k, v, cs[..., :32], cs[..., :32], 8)   # cos width
+    with pytest.raises(ValueError):
+        cache.rope_append_hot(0, q, k, v, cs.cpu(), cs.cpu(), 8)   # device
+    cache.rope_append_hot(0, q, k, v, cs, cs, 8)
+    with pytest.raises(RuntimeError):
+        cache.rope_append_hot(0, q, k, v, cs, cs, 8)               # twice in one step
