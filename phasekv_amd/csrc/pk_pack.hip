@@ -168,67 +168,91 @@ quantize_groups_kernel(QuantParams p) {
 // ---------------------------------------------------------------------------
 typedef uint32_t pk_u4 __attribute__((ext_vector_type(4)));
 
-template <int BITS>
-__device__ __forceinline__ void pack32(const float (&v)[32], const GroupStats& s,
-                                       uint32_t (&w)[BITS]) {
-  constexpr int per = 32 / BITS;            // codes per 32-bit word
+// The 32 values of a group are spread over a lane quad (quarter = lane & 3,
+// tokens or channels 8q .. 8q + 7), so a launch has four times the waves of a
+// thread-per-group kernel and each wave fewer loads in its chain.  Min / max:
+// each lane folds its eight values in order, then the quad combines them as
+// ((0, 1), (2, 3)) with the earlier quarter on the left.  nan_min / nan_max keep
+// their left operand on ties and take a NaN right operand, so this tree picks
+// the same element (sign of zero and NaN included) as the sequential fold over
+// all 32 values.  Quarter q then packs its eight codes into bytes
+// q * BITS .. q * BITS + BITS - 1 of the group (LSB-first along the group).
+__device__ __forceinline__ void quad_minmax(float& mn, float& mx, int quarter) {
 #pragma unroll
-  for (int k = 0; k < BITS; ++k) {
-    uint32_t x = 0;
-#pragma unroll
-    for (int j = 0; j < per; ++j) x |= quant_code(v[k * per + j], s, BITS) << (j * BITS);
-    w[k] = x;
+  for (int o = 1; o <= 2; o <<= 1) {
+    const float pmn = __shfl_xor(mn, o), pmx = __shfl_xor(mx, o);
+    const bool first = (quarter & o) == 0;
+    mn = first ? nan_min(mn, pmn) : nan_min(pmn, mn);
+    mx = first ? nan_max(mx, pmx) : nan_max(pmx, mx);
   }
 }
 
-__device__ __forceinline__ GroupStats stats32(const float (&v)[32], int bits) {
+__device__ __forceinline__ GroupStats quad_stats(const float (&v)[8], int quarter, int bits) {
   float mn = v[0], mx = v[0];
 #pragma unroll
-  for (int i = 1; i < 32; ++i) {
+  for (int i = 1; i < 8; ++i) {
     mn = nan_min(mn, v[i]);
     mx = nan_max(mx, v[i]);
   }
+  quad_minmax(mn, mx, quarter);
   return pk::group_stats_from(mn, mx, bits);
 }
 
-// Groups along the contiguous axis (V, per token along head_dim): one thread
-// per (row, group) with the group index fastest, four 16-byte loads, one
-// packed store.
+template <int BITS>
+__device__ __forceinline__ uint64_t pack8(const float (&v)[8], const GroupStats& s) {
+  uint64_t x = 0;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) x |= static_cast<uint64_t>(quant_code(v[t], s, BITS)) << (t * BITS);
+  return x;
+}
+
+// BITS bytes of one quarter (dst is BITS-aligned for 2 and 4 bits, 4-aligned for 8)
+template <int BITS>
+__device__ __forceinline__ void store_quarter(uint8_t* dst, uint64_t x) {
+  if constexpr (BITS == 2) {
+    *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(x);
+  } else if constexpr (BITS == 4) {
+    *reinterpret_cast<uint32_t*>(dst) = static_cast<uint32_t>(x);
+  } else {
+    reinterpret_cast<uint32_t*>(dst)[0] = static_cast<uint32_t>(x);
+    reinterpret_cast<uint32_t*>(dst)[1] = static_cast<uint32_t>(x >> 32);
+  }
+}
+
+// Groups along the contiguous axis (V, per token along head_dim): a lane quad
+// per (row, group), the group index fastest; each lane one 16-byte load.
 template <int BITS>
 __global__ void __launch_bounds__(kThreads)
 quantize_inner32_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t len, int64_t ngroups,
                         int64_t nbytes, uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
                         uint16_t* __restrict__ mins) {
-  const int64_t total = rows * ngroups;
+  const int64_t total = rows * ngroups * 4;     // whole quads: every quad runs one iteration
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / ngroups, g = i - r * ngroups;
-    const pk_u4* src = reinterpret_cast<const pk_u4*>(x + r * len + g * 32);
-    float v[32];
+    const int quarter = (int)(i & 3);
+    const int64_t j = i >> 2;
+    const int64_t r = j / ngroups, g = j - r * ngroups;
+    const pk_u4 q = *reinterpret_cast<const pk_u4*>(x + r * len + g * 32 + quarter * 8);
+    float v[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const pk_u4 q = src[k];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[8 * k + 2 * j] = pk_h2f((uint16_t)(q[j] & 0xFFFFu));
-        v[8 * k + 2 * j + 1] = pk_h2f((uint16_t)(q[j] >> 16));
-      }
+      v[2 * k] = pk_h2f((uint16_t)(q[k] & 0xFFFFu));
+      v[2 * k + 1] = pk_h2f((uint16_t)(q[k] >> 16));
     }
-    const GroupStats st = stats32(v, BITS);
-    scale[i] = pk_f2h(st.scale);
-    mins[i] = pk_f2h(st.mn);
-    uint32_t w[BITS];
-    pack32<BITS>(v, st, w);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(packed + r * nbytes + g * 4 * BITS);
-#pragma unroll
-    for (int k = 0; k < BITS; ++k) dst[k] = w[k];
+    const GroupStats st = quad_stats(v, quarter, BITS);
+    if (quarter == 0) {
+      scale[j] = pk_f2h(st.scale);
+      mins[j] = pk_f2h(st.mn);
+    }
+    store_quarter<BITS>(packed + r * nbytes + g * 4 * BITS + quarter * BITS, pack8<BITS>(v, st));
   }
 }
 
 // Groups along the second-innermost axis with a contiguous innermost dim D
-// (K, per channel along tokens): one thread per (outer, group, channel pair),
-// channel pair fastest, so each load instruction of a wave reads whole token
-// rows; each thread stores two channels' packed group and metadata.
+// (K, per channel along tokens): a lane quad per (outer, group, channel pair),
+// quarter fastest, then the channel pair, so each load instruction of a wave
+// reads 64-byte runs of four token rows; each quad stores two channels' packed
+// group and metadata.
 template <int BITS>
 __global__ void __launch_bounds__(kThreads)
 quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t len, int64_t D,
@@ -236,44 +260,46 @@ quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t l
                         uint16_t* __restrict__ scale, uint16_t* __restrict__ mins, int meta_gm,
                         int codes_tm) {
   const int64_t pairs = D / 2;
-  const int64_t total = outer * ngroups * pairs;
+  const int64_t total = outer * ngroups * pairs * 4;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t cp = i % pairs;
-    const int64_t rest = i / pairs;
-    const int64_t g = rest % ngroups, o = rest / ngroups;
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(x + (o * len + g * 32) * D + 2 * cp);
-    float a[32], b[32];
+    const int quarter = (int)(i & 3);
+    const int64_t rest = i >> 2;
+    const int64_t cp = rest % pairs;
+    const int64_t rest2 = rest / pairs;
+    const int64_t g = rest2 % ngroups, o = rest2 / ngroups;
+    const uint32_t* src =
+        reinterpret_cast<const uint32_t*>(x + (o * len + g * 32 + quarter * 8) * D + 2 * cp);
+    float a[8], b[8];
 #pragma unroll
-    for (int t = 0; t < 32; ++t) {
+    for (int t = 0; t < 8; ++t) {
       const uint32_t q = src[t * (D / 2)];
       a[t] = pk_h2f((uint16_t)(q & 0xFFFFu));
       b[t] = pk_h2f((uint16_t)(q >> 16));
     }
-    uint32_t w2[2][BITS];
+    uint64_t code[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const float (&v)[32] = k ? b : a;
-      const GroupStats st = stats32(v, BITS);
+      const float (&v)[8] = k ? b : a;
+      const GroupStats st = quad_stats(v, quarter, BITS);
       const int64_t row = o * D + 2 * cp + k;
-      const int64_t mi = meta_gm ? (o * ngroups + g) * D + 2 * cp + k : row * ngroups + g;
-      scale[mi] = pk_f2h(st.scale);
-      mins[mi] = pk_f2h(st.mn);
-      pack32<BITS>(v, st, w2[k]);
-      if (!codes_tm) {
-        uint32_t* dst = reinterpret_cast<uint32_t*>(packed + row * nbytes + g * 4 * BITS);
-#pragma unroll
-        for (int j = 0; j < BITS; ++j) dst[j] = w2[k][j];
+      if (quarter == 0) {
+        const int64_t mi = meta_gm ? (o * ngroups + g) * D + 2 * cp + k : row * ngroups + g;
+        scale[mi] = pk_f2h(st.scale);
+        mins[mi] = pk_f2h(st.mn);
       }
+      code[k] = pack8<BITS>(v, st);
+      if (!codes_tm)
+        store_quarter<BITS>(packed + row * nbytes + g * 4 * BITS + quarter * BITS, code[k]);
     }
     if (codes_tm) {
-      // byte j of the group for both channels: one 2-byte store into [bytes][D]
-      uint8_t* base = packed + (o * nbytes + g * 4 * BITS) * D + 2 * cp;
+      // byte jj of the quarter for both channels: one 2-byte store into [bytes][D]
+      uint8_t* base = packed + (o * nbytes + g * 4 * BITS + quarter * BITS) * D + 2 * cp;
 #pragma unroll
-      for (int j = 0; j < 4 * BITS; ++j) {
-        const uint32_t lo = (w2[0][j >> 2] >> (8 * (j & 3))) & 0xFFu;
-        const uint32_t hi = (w2[1][j >> 2] >> (8 * (j & 3))) & 0xFFu;
-        *reinterpret_cast<uint16_t*>(base + (int64_t)j * D) = (uint16_t)(lo | (hi << 8));
+      for (int jj = 0; jj < BITS; ++jj) {
+        const uint32_t lo = static_cast<uint32_t>(code[0] >> (8 * jj)) & 0xFFu;
+        const uint32_t hi = static_cast<uint32_t>(code[1] >> (8 * jj)) & 0xFFu;
+        *reinterpret_cast<uint16_t*>(base + (int64_t)jj * D) = (uint16_t)(lo | (hi << 8));
       }
     }
   }
@@ -458,8 +484,8 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
   const bool fast = dtype == PK_DTYPE_F16 && contiguous && group_size == 32 && p.len % 32 == 0 &&
                     reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if (fast && axis == ndim - 1 && !layout) {
-    const int64_t groups = p.rows * p.ngroups;
-#define PK_INNER(B) hipLaunchKernelGGL(quantize_inner32_kernel<B>, dim3(grid_for(groups)), dim3(kThreads), \
+    const int64_t lanes = p.rows * p.ngroups * 4;
+#define PK_INNER(B) hipLaunchKernelGGL(quantize_inner32_kernel<B>, dim3(grid_for(lanes)), dim3(kThreads), \
                                        0, s, static_cast<const uint16_t*>(x), p.rows, p.len, p.ngroups, \
                                        p.nbytes, out_packed, out_scale, out_mins)
     if (bits == 2) PK_INNER(2); else if (bits == 4) PK_INNER(4); else PK_INNER(8);
@@ -469,7 +495,7 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
   if (fast && axis == ndim - 2 && shape[ndim - 1] % 2 == 0) {
     const int64_t D = shape[ndim - 1];
     const int64_t outer = p.rows / D;
-    const int64_t threads = outer * p.ngroups * (D / 2);
+    const int64_t threads = outer * p.ngroups * (D / 2) * 4;
 #define PK_OUTER(B) hipLaunchKernelGGL(quantize_outer32_kernel<B>, dim3(grid_for(threads)), dim3(kThreads), \
                                        0, s, static_cast<const uint16_t*>(x), outer, p.len, D, p.ngroups, \
                                        p.nbytes, out_packed, out_scale, out_mins, p.meta_gm, p.codes_tm)
