@@ -202,6 +202,19 @@ int pk_append_hot(const uint16_t* k_src, const uint16_t* v_src, int64_t k_bstrid
                   int64_t hot_tstride, int batch, int num_kv_heads, int head_dim,
                   int64_t position, int64_t capacity, void* stream);
 
+/* Write `count` consecutive tokens' K and V (fp16 [batch, num_kv_heads, count,
+ * head_dim], element strides of batch, head and token given, head_dim
+ * contiguous) into rows position .. position + count - 1 of the hot window
+ * (layout as pk_append_hot).  Fails unless 0 <= position and position + count
+ * <= capacity.  Replaces the per-token append_hot loop over an input chunk
+ * (src/phasekv/qwen2_attention.py:100-106, phasekv_cache.py:344-390). */
+int pk_append_hot_rows(const uint16_t* k_src, const uint16_t* v_src, int64_t k_bstride,
+                       int64_t k_hstride, int64_t k_tstride, int64_t v_bstride,
+                       int64_t v_hstride, int64_t v_tstride, uint16_t* hot_k, uint16_t* hot_v,
+                       int64_t hot_bstride, int64_t hot_hstride, int64_t hot_tstride,
+                       int batch, int num_kv_heads, int head_dim, int64_t position,
+                       int64_t count, int64_t capacity, void* stream);
+
 /* One decode token's rotate_half rotary embedding fused with the window append.
  * q (fp16 [batch][num_q_heads * head_dim], batch stride q_bstride) is rotated
  * into q_out (fp16 [batch, num_q_heads, head_dim], contiguous); K (same layout

@@ -102,6 +102,10 @@ _SIGNATURES = {
     "pk_append_hot": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,
                                      _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_int, _c_i64, _c_i64, _c_vp]),
+    "pk_append_hot_rows": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                          _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_i64,
+                                          _c_i64, _c_i64, _c_vp]),
     "pk_rope_append_hot": (ctypes.c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp,
                                           _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,

@@ -21,7 +21,8 @@ decode loop:
 
 * multi-turn prompt chunks ``begin_prompt_chunk`` / ``append_prompt_token`` /
   ``finish_prompt_chunk`` (``:342-403``): the chunk borrows the hot window, and is packed
-  with ``prompt_bits`` into a prompt extension at its end
+  with ``prompt_bits`` into a prompt extension at its end; ``append_prompt_chunk``
+  writes a layer's chunk rows in one launch
 * ``reorder_cache`` (``:454-478``): batch reorder of every tier, keeping the transposed
   K storage ``quantize_pack`` gives
 
@@ -492,6 +493,46 @@ class PhaseKVCache:
             raise RuntimeError(f"layer {layer_idx} already holds the chunk's "
                                f"{self._prompt_chunk_len} tokens")
         self._append_token(layer_idx, layer, key, value)
+
+    @torch.no_grad()
+    def append_prompt_chunk(self, layer_idx: int, key: torch.Tensor, value: torch.Tensor) -> None:
+        """The next ``T`` chunk tokens of one layer (``[B, Hkv, T, hd]`` fp16) in one launch:
+        the window rows equal ``T`` calls of ``append_prompt_token``
+        (``qwen2_attention.py:100-106``).  Causality comes from the chunk attention's
+        per-row lengths, as with the per-token appends."""
+        if not self._prompt_chunk_len:
+            raise RuntimeError("no prompt chunk is open; call begin_prompt_chunk(length) first")
+        layer = self.layer_tiers(layer_idx)
+        context = f"layer {layer_idx} chunk K/V"
+        if not isinstance(key, torch.Tensor) or not isinstance(value, torch.Tensor):
+            raise TypeError(f"{context} must be tensors")
+        hk, hv = layer.hot_k, layer.hot_v
+        B, hkv, cap, hd = hk.shape
+        if key.dim() != 4 or key.shape != value.shape or tuple(key.shape[:2]) != (B, hkv) \
+                or key.shape[3] != hd or key.shape[2] <= 0:
+            raise ValueError(f"{context} must be [B, Hkv, T, hd] = [{B}, {hkv}, T, {hd}], got "
+                             f"{tuple(key.shape)}/{tuple(value.shape)}")
+        if key.dtype != torch.float16 or value.dtype != torch.float16:
+            raise ValueError(f"{context} must be float16, got {key.dtype}/{value.dtype}")
+        if key.device != hk.device or value.device != hv.device:
+            raise ValueError(f"{context} must be on the hot window's device {hk.device}")
+        count = key.shape[2]
+        written = layer.hot_len - self._prompt_chunk_start[layer_idx]
+        if written + count > self._prompt_chunk_len:
+            raise RuntimeError(f"layer {layer_idx} holds {written} of the chunk's "
+                               f"{self._prompt_chunk_len} tokens; {count} more do not fit")
+        if hk.stride() != hv.stride() or hk.stride(-1) != 1:
+            raise ValueError("hot_k and hot_v must share strides with a contiguous head_dim")
+        if key.stride(-1) != 1:
+            key = key.contiguous()
+        if value.stride(-1) != 1:
+            value = value.contiguous()
+        _lib.check(_lib.load().pk_append_hot_rows(
+            key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), key.stride(2),
+            value.stride(0), value.stride(1), value.stride(2), hk.data_ptr(), hv.data_ptr(),
+            hk.stride(0), hk.stride(1), hk.stride(2), B, hkv, hd, layer.hot_len, count, cap,
+            _lib.stream_ptr(hk.device)), "append_hot_rows")
+        layer.hot_len += count
 
     @torch.no_grad()
     def finish_prompt_chunk(self) -> None:

@@ -26,20 +26,25 @@ struct HotView {
 };
 
 // ---------------------------------------------------------------------------
-// append: hot[b, h, position, :] = src[b, h, 0, :] for K and V
+// append: hot[b, h, position + t, :] = src[b, h, t, :] for K and V, t < count
 // ---------------------------------------------------------------------------
+struct SrcView {
+  int64_t bs, hs, ts;   // element strides of batch, kv head, token; head_dim is contiguous
+};
+
 __global__ void __launch_bounds__(kCoolThreads)
-append_hot_kernel(const uint16_t* __restrict__ ks, const uint16_t* __restrict__ vs,
-                  int64_t ksb, int64_t ksh, int64_t vsb, int64_t vsh, uint16_t* hk, uint16_t* hv,
-                  HotView hot, int Hkv, int hd, int64_t position, int64_t total) {
+append_hot_kernel(const uint16_t* __restrict__ ks, const uint16_t* __restrict__ vs, SrcView kv,
+                  SrcView vv, uint16_t* hk, uint16_t* hv, HotView hot, int Hkv, int hd,
+                  int64_t position, int64_t count, int64_t total) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = i / hd;
     const int c = (int)(i - row * hd);
-    const int64_t b = row / Hkv, h = row - b * Hkv;
-    const int64_t dst = b * hot.bs + h * hot.hs + position * hot.ts + c;
-    hk[dst] = ks[b * ksb + h * ksh + c];
-    hv[dst] = vs[b * vsb + h * vsh + c];
+    const int64_t bh = row / count, t = row - bh * count;
+    const int64_t b = bh / Hkv, h = bh - b * Hkv;
+    const int64_t dst = b * hot.bs + h * hot.hs + (position + t) * hot.ts + c;
+    hk[dst] = ks[b * kv.bs + h * kv.hs + t * kv.ts + c];
+    hv[dst] = vs[b * vv.bs + h * vv.hs + t * vv.ts + c];
   }
 }
 
@@ -447,11 +452,37 @@ extern "C" int pk_append_hot(const uint16_t* k_src, const uint16_t* v_src, int64
   const int64_t total = (int64_t)batch * num_kv_heads * head_dim;
   const int grid = (int)std::min<int64_t>(pk::cdiv(total, kCoolThreads), 4096);
   hipLaunchKernelGGL(append_hot_kernel, dim3(grid), dim3(kCoolThreads), 0,
-                     static_cast<hipStream_t>(stream), k_src, v_src, k_bstride, k_hstride,
-                     v_bstride, v_hstride, hot_k, hot_v,
-                     HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
-                     position, total);
+                     static_cast<hipStream_t>(stream), k_src, v_src,
+                     SrcView{k_bstride, k_hstride, 0}, SrcView{v_bstride, v_hstride, 0}, hot_k,
+                     hot_v, HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads,
+                     head_dim, position, (int64_t)1, total);
   return pk::check_launch("append_hot");
+}
+
+extern "C" int pk_append_hot_rows(const uint16_t* k_src, const uint16_t* v_src, int64_t k_bstride,
+                                  int64_t k_hstride, int64_t k_tstride, int64_t v_bstride,
+                                  int64_t v_hstride, int64_t v_tstride, uint16_t* hot_k,
+                                  uint16_t* hot_v, int64_t hot_bstride, int64_t hot_hstride,
+                                  int64_t hot_tstride, int batch, int num_kv_heads, int head_dim,
+                                  int64_t position, int64_t count, int64_t capacity,
+                                  void* stream) {
+  pk::clear_error();
+  if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
+                         hot_tstride))
+    return rc;
+  if (!k_src || !v_src) return pk::fail("null K/V source");
+  if (count <= 0) return pk::fail("count must be positive");
+  if (position < 0 || position > capacity - count)
+    return pk::fail("the rows do not fit in the hot window");
+  const int64_t total = (int64_t)batch * num_kv_heads * count * head_dim;
+  const int grid = (int)std::min<int64_t>(pk::cdiv(total, kCoolThreads), 4096);
+  hipLaunchKernelGGL(append_hot_kernel, dim3(grid), dim3(kCoolThreads), 0,
+                     static_cast<hipStream_t>(stream), k_src, v_src,
+                     SrcView{k_bstride, k_hstride, k_tstride},
+                     SrcView{v_bstride, v_hstride, v_tstride}, hot_k, hot_v,
+                     HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
+                     position, count, total);
+  return pk::check_launch("append_hot_rows");
 }
 
 extern "C" int pk_rope_append_hot(const uint16_t* q, int64_t q_bstride, const uint16_t* k,

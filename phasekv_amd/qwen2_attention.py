@@ -90,8 +90,7 @@ class PhaseKVAttention(nn.Module):
         q, k, v = q.to(torch.float16), k.to(torch.float16), v.to(torch.float16)
         tiers = cache.layer_tiers(self.layer_idx)
         if cache.prompt_chunk_len:
-            for i in range(q_len):
-                cache.append_prompt_token(self.layer_idx, k[:, :, i:i + 1], v[:, :, i:i + 1])
+            cache.append_prompt_chunk(self.layer_idx, k, v)
             out = fused_phasekv_prompt_chunk_attention(q[0].transpose(0, 1).contiguous(), tiers, hq)
         else:
             cache.append_hot(self.layer_idx, k, v)

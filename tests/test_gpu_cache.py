@@ -433,3 +433,43 @@ def test_rope_append_hot_errors(gpu):
     cache.rope_append_hot(0, q, k, v, cs, cs, 8)
     with pytest.raises(RuntimeError):
         cache.rope_append_hot(0, q, k, v, cs, cs, 8)               # twice in one step
+
+
+def test_append_prompt_chunk_matches_per_token_appends(gpu):
+    """One ``pk_append_hot_rows`` launch per layer writes the same window rows as the
+    per-token loop, in one call or two (3 + 6 rows, strided sources), and refuses rows
+    beyond the chunk."""
+    from phasekv_amd.cache import PhaseKVCache
+    g = torch.Generator().manual_seed(21)
+    B, H, hd, S, T = 2, 2, 128, 64, 9
+    dense = _Dense([torch.randn(B, H, S, hd, generator=g).to(torch.float16).to(gpu)],
+                   [torch.randn(B, H, S, hd, generator=g).to(torch.float16).to(gpu)])
+    caches = [PhaseKVCache.from_dense_prefill(dense, prompt_len=S, prompt_bits=4, cold_bits=4,
+                                              group_size=32, recent_window=32, lazy_g=16)
+              for _ in range(3)]
+    gen = [torch.randn(B, H, 1, hd, generator=g).to(torch.float16).to(gpu) for _ in range(5)]
+    for c in caches:          # the same generated tokens in every window first
+        for k in gen:
+            c.append_hot(0, k, k * 2)
+            c.finish_decode_step()
+    k = torch.randn(B, T, H, hd, generator=g).to(torch.float16).to(gpu).transpose(1, 2)  # strided
+    v = torch.randn(B, H, T, hd, generator=g).to(torch.float16).to(gpu)
+    for c in caches:
+        c.begin_prompt_chunk(T)
+    for t in range(T):
+        caches[0].append_prompt_token(0, k[:, :, t:t + 1], v[:, :, t:t + 1])
+    caches[1].append_prompt_chunk(0, k, v)
+    caches[2].append_prompt_chunk(0, k[:, :, :3], v[:, :, :3])
+    caches[2].append_prompt_chunk(0, k[:, :, 3:], v[:, :, 3:])
+    with pytest.raises(RuntimeError):
+        caches[2].append_prompt_chunk(0, k[:, :, :1], v[:, :, :1])
+    want_k, want_v = caches[0].layer_tiers(0).hot_views()
+    for c in caches[1:]:
+        got_k, got_v = c.layer_tiers(0).hot_views()
+        assert torch.equal(got_k, want_k) and torch.equal(got_v, want_v)
+    for c in caches:
+        c.finish_prompt_chunk()
+    ext = [c.layer_tiers(0).prompt_extensions[-1] for c in caches]
+    for e in ext[1:]:
+        assert torch.equal(e.key.packed, ext[0].key.packed)
+        assert torch.equal(e.value.packed, ext[0].value.packed)
