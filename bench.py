@@ -324,11 +324,30 @@ def _bench_e2e(device, prompt_len, layers, steps):
             model(toks[i:i + 1], past_key_values=dense, use_cache=True)
         torch.cuda.synchronize()
         dn = (time.perf_counter() - t0) / steps
+        # a new input chunk of 64 tokens (a follow-up turn), 4 in a row: the adapter appends,
+        # attends in one chunk launch per layer and packs the chunk into a prompt extension
+        chunk_t, chunks = 64, 4
+        cids = torch.randint(0, cfg.vocab_size, (chunks + 1, chunk_t), generator=gen).to(device)
+        phasekv_step(model, cids[:1], cache)                       # untimed first chunk
+        model(cids[:1], past_key_values=dense, use_cache=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(1, chunks + 1):
+            phasekv_step(model, cids[i:i + 1], cache)
+        torch.cuda.synchronize()
+        pk_chunk = (time.perf_counter() - t0) / chunks
+        t0 = time.perf_counter()
+        for i in range(1, chunks + 1):
+            model(cids[i:i + 1], past_key_values=dense, use_cache=True)
+        torch.cuda.synchronize()
+        dn_chunk = (time.perf_counter() - t0) / chunks
     del model, cache, dense
     torch.cuda.empty_cache()
     return {"config": f"e2e-qwen2.5-7b-shape-{layers}L", "prompt_len": prompt_len,
             "phasekv_ms_per_token": pk * 1e3, "dense_ms_per_token": dn * 1e3,
-            "speedup_vs_dense": dn / pk}
+            "speedup_vs_dense": dn / pk, "chunk_tokens": chunk_t,
+            "phasekv_ms_per_chunk": pk_chunk * 1e3, "dense_ms_per_chunk": dn_chunk * 1e3,
+            "chunk_speedup_vs_dense": dn_chunk / pk_chunk}
 
 
 def _cpu_baseline(cfg_name: str, budget_s: float = 10.0):
