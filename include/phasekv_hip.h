@@ -216,19 +216,20 @@ int pk_append_hot_rows(const uint16_t* k_src, const uint16_t* v_src, int64_t k_b
                        int64_t count, int64_t capacity, void* stream);
 
 /* One decode token's rotate_half rotary embedding fused with the window append.
- * q (fp16 [batch][num_q_heads * head_dim], batch stride q_bstride) is rotated
- * into q_out (fp16 [batch, num_q_heads, head_dim], contiguous); K (same layout
- * with num_kv_heads, batch stride kv_bstride, shared by V) is rotated into row
- * `position` of the hot window and V is copied there.  cos / sin: fp16
- * [batch][head_dim], batch stride cs_bstride (0: one row for every batch row).
- * Each output is x * cos + rotate_half(x) * sin evaluated on fp16 values (each
- * product and the sum rounded to fp16), bit-identical to that expression on
- * fp16 tensors.  Replaces apply_rotary_pos_emb followed by append_hot in the
- * adapters' decode branch (src/phasekv/qwen2_attention.py:89-92, 77;
- * examples/llama_phasekv_adapter.py:71-74, 89). */
+ * Inputs are of `dtype` (PK_DTYPE_F16 or PK_DTYPE_BF16).  q ([batch][num_q_heads
+ * * head_dim], batch stride q_bstride) is rotated into q_out (fp16 [batch,
+ * num_q_heads, head_dim], contiguous); K (same layout with num_kv_heads, batch
+ * stride kv_bstride, shared by V) is rotated into row `position` of the fp16 hot
+ * window and V is copied there.  cos / sin: [batch][head_dim], batch stride
+ * cs_bstride (0: one row for every batch row).  Each output is
+ * x * cos + rotate_half(x) * sin evaluated in `dtype` (each product and the sum
+ * rounded to it), then rounded to fp16: bit-identical to that expression on
+ * tensors of `dtype` followed by `.to(float16)`.  Replaces apply_rotary_pos_emb,
+ * the fp16 casts and append_hot in the adapters' decode branch
+ * (src/phasekv/qwen2_attention.py:89-92, 77; examples/llama_phasekv_adapter.py:71-74, 89). */
 int pk_rope_append_hot(const uint16_t* q, int64_t q_bstride, const uint16_t* k,
                        const uint16_t* v, int64_t kv_bstride, const uint16_t* cos,
-                       const uint16_t* sin, int64_t cs_bstride, uint16_t* q_out,
+                       const uint16_t* sin, int64_t cs_bstride, int dtype, uint16_t* q_out,
                        uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride,
                        int64_t hot_hstride, int64_t hot_tstride, int batch, int num_q_heads,
                        int num_kv_heads, int head_dim, int64_t position, int64_t capacity,

@@ -107,7 +107,8 @@ _SIGNATURES = {
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_i64,
                                           _c_i64, _c_i64, _c_vp]),
     "pk_rope_append_hot": (ctypes.c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp,
-                                          _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                          _c_i64, ctypes.c_int, _c_vp, _c_vp, _c_vp, _c_i64,
+                                          _c_i64, _c_i64,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           _c_i64, _c_i64, _c_vp]),
     "pk_cool_hot": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,

@@ -329,14 +329,14 @@ class PhaseKVCache:
     def rope_append_hot(self, layer_idx: int, query: torch.Tensor, key: torch.Tensor,
                         value: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                         num_attention_heads: int) -> torch.Tensor:
-        """``apply_rotary_pos_emb`` (rotate_half form) and ``append_hot`` of one decode
-        token in one launch; returns the rotated query ``[B, Hq, hd]`` fp16.
+        """``apply_rotary_pos_emb`` (rotate_half form), the fp16 casts and ``append_hot``
+        of one decode token in one launch; returns the rotated query ``[B, Hq, hd]`` fp16.
 
-        ``query`` / ``key`` / ``value`` are the fp16 projections ``[B, 1, H*hd]`` (head_dim
-        contiguous), ``cos`` / ``sin`` fp16 ``[B or 1, 1, hd]``.  The rotated K and the V
-        go into the window as ``append_hot`` writes them, bit-identical to rotating the
-        fp16 tensors with ``x * cos + rotate_half(x) * sin`` first
-        (``qwen2_attention.py:89-92, 77``).
+        ``query`` / ``key`` / ``value`` are the projections ``[B, 1, H*hd]`` (head_dim
+        contiguous) and ``cos`` / ``sin`` ``[B or 1, 1, hd]``, all float16 or all
+        bfloat16.  The rotated K and the V go into the window as ``append_hot`` writes
+        them, bit-identical to ``x * cos + rotate_half(x) * sin`` on the tensors
+        followed by ``.to(torch.float16)`` (``qwen2_attention.py:89-92, 77``).
         """
         if self._prompt_chunk_len:
             raise RuntimeError("a prompt chunk is open: append with append_prompt_token() and "
@@ -351,8 +351,10 @@ class PhaseKVCache:
         tensors = (query, key, value, cos, sin)
         if not all(isinstance(t, torch.Tensor) for t in tensors):
             raise TypeError(f"layer {layer_idx} query / key / value / cos / sin must be tensors")
-        if any(t.dtype != torch.float16 for t in tensors):
-            raise ValueError(f"layer {layer_idx} query / key / value / cos / sin must be float16")
+        dtype = query.dtype
+        if dtype not in (torch.float16, torch.bfloat16) or any(t.dtype != dtype for t in tensors):
+            raise ValueError(f"layer {layer_idx} query / key / value / cos / sin must be all "
+                             "float16 or all bfloat16")
         if hq <= 0 or hq % hkv:
             raise ValueError(f"num_attention_heads {hq} must be a positive multiple of {hkv}")
         if (tuple(query.shape) != (B, 1, hq * hd) or tuple(key.shape) != (B, 1, hkv * hd)
@@ -384,7 +386,9 @@ class PhaseKVCache:
         kv_bstride = key.stride(0) if B > 1 else hkv * hd
         _lib.check(_lib.load().pk_rope_append_hot(
             query.data_ptr(), q_bstride, key.data_ptr(), value.data_ptr(), kv_bstride,
-            cos.data_ptr(), sin.data_ptr(), cs_bstride, q_out.data_ptr(), hk.data_ptr(),
+            cos.data_ptr(), sin.data_ptr(), cs_bstride,
+            _lib.PK_DTYPE_BF16 if dtype == torch.bfloat16 else _lib.PK_DTYPE_F16,
+            q_out.data_ptr(), hk.data_ptr(),
             hv.data_ptr(), hk.stride(0), hk.stride(1), hk.stride(2), B, hq, hkv, hd,
             layer.hot_len, cap, _lib.stream_ptr(dev)), "rope_append_hot")
         layer.hot_len += 1

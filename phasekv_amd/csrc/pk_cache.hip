@@ -50,17 +50,37 @@ append_hot_kernel(const uint16_t* __restrict__ ks, const uint16_t* __restrict__ 
 
 // One decode token's rotary embedding, fused with the window append: thread
 // (row, d) with d < hd/2 rotates the pair (d, d + hd/2) of one q head or one
-// kv head.  The arithmetic is the fp16 sequence of rotate_half RoPE,
-// x * cos + rotate_half(x) * sin, each product and the sum computed in float
-// and rounded to fp16 (so the result equals that expression on fp16 tensors).
-// q heads go to q_out [B, Hq, hd]; k heads are rotated into the window at
-// `position`, v heads are copied there.
-__device__ __forceinline__ uint16_t rope_half(float x, float c, float r, float sn) {
-  const float a = pk_h2f(pk_f2h(x * c));
-  const float b = pk_h2f(pk_f2h(r * sn));
-  return pk_f2h(a + b);
+// kv head.  The arithmetic is the sequence of rotate_half RoPE on tensors of
+// the model's dtype T (fp16 or bf16), x * cos + rotate_half(x) * sin: each
+// product and the sum computed in float and rounded to T.  The results are
+// then rounded to fp16 (exact for fp16; for bf16 the cast `.to(float16)` that
+// feeds the fp16 cache).  q heads go to q_out [B, Hq, hd] fp16; k heads are
+// rotated into the window at `position`, v heads converted and copied there.
+template <bool BF16>
+__device__ __forceinline__ float rope_load(uint16_t h) { return BF16 ? pk_bf2f(h) : pk_h2f(h); }
+
+// float -> bf16, round to nearest even; NaN becomes the quiet NaN 0x7FC0, as
+// torch's conversion does
+__device__ __forceinline__ float round_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return __uint_as_float(0x7FC00000u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xFFFF0000u);
 }
 
+template <bool BF16>
+__device__ __forceinline__ float rope_round(float f) {
+  return BF16 ? round_bf16(f) : pk_h2f(pk_f2h(f));
+}
+
+template <bool BF16>
+__device__ __forceinline__ uint16_t rope_half(float x, float c, float r, float sn) {
+  const float a = rope_round<BF16>(x * c);
+  const float b = rope_round<BF16>(r * sn);
+  return pk_f2h(rope_round<BF16>(a + b));
+}
+
+template <bool BF16>
 __global__ void __launch_bounds__(256)
 rope_append_kernel(const uint16_t* __restrict__ q, int64_t qsb, const uint16_t* __restrict__ k,
                    const uint16_t* __restrict__ v, int64_t kvsb, const uint16_t* __restrict__ cs,
@@ -76,23 +96,23 @@ rope_append_kernel(const uint16_t* __restrict__ q, int64_t qsb, const uint16_t* 
     const int h = (int)(row - b * (Hq + Hkv));
     const uint16_t* cr = cs + b * csb;
     const uint16_t* sr = sn + b * csb;
-    const float c1 = pk_h2f(cr[d]), c2 = pk_h2f(cr[d + half]);
-    const float s1 = pk_h2f(sr[d]), s2 = pk_h2f(sr[d + half]);
+    const float c1 = rope_load<BF16>(cr[d]), c2 = rope_load<BF16>(cr[d + half]);
+    const float s1 = rope_load<BF16>(sr[d]), s2 = rope_load<BF16>(sr[d + half]);
     if (h < Hq) {
       const uint16_t* x = q + b * qsb + (int64_t)h * hd;
-      const float x1 = pk_h2f(x[d]), x2 = pk_h2f(x[d + half]);
+      const float x1 = rope_load<BF16>(x[d]), x2 = rope_load<BF16>(x[d + half]);
       uint16_t* o = q_out + (b * Hq + h) * (int64_t)hd;
-      o[d] = rope_half(x1, c1, -x2, s1);
-      o[d + half] = rope_half(x2, c2, x1, s2);
+      o[d] = rope_half<BF16>(x1, c1, -x2, s1);
+      o[d + half] = rope_half<BF16>(x2, c2, x1, s2);
     } else {
       const int hk_ = h - Hq;
       const int64_t src = b * kvsb + (int64_t)hk_ * hd;
-      const float x1 = pk_h2f(k[src + d]), x2 = pk_h2f(k[src + d + half]);
+      const float x1 = rope_load<BF16>(k[src + d]), x2 = rope_load<BF16>(k[src + d + half]);
       const int64_t dst = b * hot.bs + hk_ * hot.hs + position * hot.ts;
-      hk[dst + d] = rope_half(x1, c1, -x2, s1);
-      hk[dst + d + half] = rope_half(x2, c2, x1, s2);
-      hv[dst + d] = v[src + d];
-      hv[dst + d + half] = v[src + d + half];
+      hk[dst + d] = rope_half<BF16>(x1, c1, -x2, s1);
+      hk[dst + d + half] = rope_half<BF16>(x2, c2, x1, s2);
+      hv[dst + d] = BF16 ? pk_f2h(pk_bf2f(v[src + d])) : v[src + d];
+      hv[dst + d + half] = BF16 ? pk_f2h(pk_bf2f(v[src + d + half])) : v[src + d + half];
     }
   }
 }
@@ -487,7 +507,8 @@ extern "C" int pk_append_hot_rows(const uint16_t* k_src, const uint16_t* v_src, 
 
 extern "C" int pk_rope_append_hot(const uint16_t* q, int64_t q_bstride, const uint16_t* k,
                                   const uint16_t* v, int64_t kv_bstride, const uint16_t* cos,
-                                  const uint16_t* sin, int64_t cs_bstride, uint16_t* q_out,
+                                  const uint16_t* sin, int64_t cs_bstride, int dtype,
+                                  uint16_t* q_out,
                                   uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride,
                                   int64_t hot_hstride, int64_t hot_tstride, int batch,
                                   int num_q_heads, int num_kv_heads, int head_dim,
@@ -500,17 +521,26 @@ extern "C" int pk_rope_append_hot(const uint16_t* q, int64_t q_bstride, const ui
   if (num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return pk::fail("num_q_heads must be a positive multiple of num_kv_heads");
   if (head_dim % 2) return pk::fail("head_dim must be even for the rotary embedding");
+  if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16)
+    return pk::fail("q / K / V / cos / sin must be float16 or bfloat16");
   if (q_bstride < (int64_t)num_q_heads * head_dim || kv_bstride < (int64_t)num_kv_heads * head_dim ||
       cs_bstride < 0)
     return pk::fail("q / K / V batch strides must cover their heads; cos / sin stride >= 0");
   if (position < 0 || position >= capacity) return pk::fail("hot window is full");
   const int64_t total = (int64_t)batch * (num_q_heads + num_kv_heads) * (head_dim / 2);
   const int grid = (int)std::min<int64_t>(pk::cdiv(total, 256), 4096);
-  hipLaunchKernelGGL(rope_append_kernel, dim3(grid), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), q, q_bstride, k, v, kv_bstride, cos, sin,
-                     cs_bstride, q_out, hot_k, hot_v,
-                     HotView{hot_bstride, hot_hstride, hot_tstride}, num_q_heads, num_kv_heads,
-                     head_dim, position, total);
+  if (dtype == PK_DTYPE_BF16)
+    hipLaunchKernelGGL(rope_append_kernel<true>, dim3(grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), q, q_bstride, k, v, kv_bstride, cos, sin,
+                       cs_bstride, q_out, hot_k, hot_v,
+                       HotView{hot_bstride, hot_hstride, hot_tstride}, num_q_heads, num_kv_heads,
+                       head_dim, position, total);
+  else
+    hipLaunchKernelGGL(rope_append_kernel<false>, dim3(grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), q, q_bstride, k, v, kv_bstride, cos, sin,
+                       cs_bstride, q_out, hot_k, hot_v,
+                       HotView{hot_bstride, hot_hstride, hot_tstride}, num_q_heads, num_kv_heads,
+                       head_dim, position, total);
   return pk::check_launch("rope_append_hot");
 }
 

@@ -31,7 +31,7 @@ class PhaseKVAttention(nn.Module):
     chunks on a ``PhaseKVCache``.  The layer only writes K/V and attends; the caller
     calls ``finish_decode_step`` / ``finish_prompt_chunk`` after the model's forward.
     Subclasses give the model family's RoPE; ``fused_rope`` says it is the rotate_half
-    form, which an fp16 decode step applies in the window-append launch
+    form, which a decode step applies in the window-append launch
     (``PhaseKVCache.rope_append_hot``)."""
 
     fused_rope = False
@@ -74,14 +74,14 @@ class PhaseKVAttention(nn.Module):
         if position_embeddings is None:
             raise ValueError("position_embeddings (RoPE cos, sin at the true positions) are needed")
         if (self.fused_rope and not cache.prompt_chunk_len
-                and hidden_states.dtype == torch.float16
-                and position_embeddings[0].dtype == torch.float16):
-            # one launch: q and k rotated, k and v written into the window
+                and position_embeddings[0].dtype == hidden_states.dtype):
+            # one launch: q and k rotated, cast to fp16, k and v written into the window
             q = cache.rope_append_hot(self.layer_idx, base.q_proj(hidden_states),
                                       base.k_proj(hidden_states), base.v_proj(hidden_states),
                                       *position_embeddings, hq)
             out = fused_phasekv_decode(q[0], cache.layer_tiers(self.layer_idx), hq)
-            return base.o_proj(out.reshape(batch, q_len, hq * hd)), None
+            out = out.reshape(batch, q_len, hq * hd).to(hidden_states.dtype)
+            return base.o_proj(out), None
         q = base.q_proj(hidden_states).view(batch, q_len, hq, hd).transpose(1, 2)
         k = base.k_proj(hidden_states).view(batch, q_len, hkv, hd).transpose(1, 2)
         v = base.v_proj(hidden_states).view(batch, q_len, hkv, hd).transpose(1, 2)

@@ -372,15 +372,17 @@ def test_reused_decode_problem_matches_a_fresh_one(gpu):
     assert [i for i, r in enumerate(rebuilt) if r] == [0, 48, 60]
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("B,hq,hkv,hd,cos_rows,positions", [
     (1, 28, 4, 128, 1, (5, 4100, 32767)), (2, 8, 2, 64, 2, (0, 77)), (3, 12, 4, 128, 1, (1234,))])
-def test_rope_append_hot_matches_apply_rotary_pos_emb(gpu, B, hq, hkv, hd, cos_rows, positions):
-    """One launch equals transformers' ``apply_rotary_pos_emb`` on the fp16 tensors followed
-    by ``append_hot``: the rotated q and the window rows bit for bit, at short and long
-    positions, with one cos / sin row for every batch row or one per row."""
+def test_rope_append_hot_matches_apply_rotary_pos_emb(gpu, B, hq, hkv, hd, cos_rows, positions,
+                                                      dtype):
+    """One launch equals transformers' ``apply_rotary_pos_emb`` on fp16 or bf16 tensors,
+    ``.to(float16)`` and ``append_hot``: the rotated q and the window rows bit for bit, at
+    short and long positions, with one cos / sin row for every batch row or one per row."""
     from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
     from phasekv_amd.cache import PhaseKVCache
-    print(f"case B={B} hq={hq} hkv={hkv} hd={hd} cos_rows={cos_rows}", flush=True)
+    print(f"case B={B} hq={hq} hkv={hkv} hd={hd} cos_rows={cos_rows} {dtype}", flush=True)
     g = torch.Generator().manual_seed(B * 100 + hd)
     S = 40
     dense = _Dense([torch.randn(B, hkv, S, hd, generator=g).to(torch.float16).to(gpu)],
@@ -394,16 +396,17 @@ def test_rope_append_hot_matches_apply_rotary_pos_emb(gpu, B, hq, hkv, hd, cos_r
         p = torch.tensor([pos + r for r in range(cos_rows)], dtype=torch.float32)
         freqs = p[:, None] * inv[None, :]
         emb = torch.cat((freqs, freqs), dim=-1)
-        cos = emb.cos().to(torch.float16)[:, None, :].to(gpu)
-        sin = emb.sin().to(torch.float16)[:, None, :].to(gpu)
-        q = (torch.randn(B, 1, hq * hd, generator=g) * 4).to(torch.float16).to(gpu)
-        k = (torch.randn(B, 1, hkv * hd, generator=g) * 4).to(torch.float16).to(gpu)
-        v = torch.randn(B, 1, hkv * hd, generator=g).to(torch.float16).to(gpu)
+        cos = emb.cos().to(dtype)[:, None, :].to(gpu)
+        sin = emb.sin().to(dtype)[:, None, :].to(gpu)
+        q = (torch.randn(B, 1, hq * hd, generator=g) * 4).to(dtype).to(gpu)
+        k = (torch.randn(B, 1, hkv * hd, generator=g) * 4).to(dtype).to(gpu)
+        v = torch.randn(B, 1, hkv * hd, generator=g).to(dtype).to(gpu)
         got_q = fused.rope_append_hot(0, q, k, v, cos, sin, hq)
         qh = q.view(B, 1, hq, hd).transpose(1, 2)
         kh = k.view(B, 1, hkv, hd).transpose(1, 2)
         want_q, want_k = apply_rotary_pos_emb(qh, kh, cos, sin)
-        plain.append_hot(0, want_k, v.view(B, 1, hkv, hd).transpose(1, 2))
+        want_q, want_k = want_q.to(torch.float16), want_k.to(torch.float16)
+        plain.append_hot(0, want_k, v.view(B, 1, hkv, hd).transpose(1, 2).to(torch.float16))
         assert torch.equal(got_q, want_q[:, :, 0, :]), f"q at position {pos}"
         fk, fv = fused.layer_tiers(0).hot_views()
         pk_, pv = plain.layer_tiers(0).hot_views()
@@ -426,6 +429,8 @@ def test_rope_append_hot_errors(gpu):
         cache.rope_append_hot(0, q, k, v, cs, cs, 6)               # q is not [1, 1, 6 * 64]
     with pytest.raises(ValueError):
         cache.rope_append_hot(0, q.float(), k, v, cs, cs, 8)       # dtype
+    with pytest.raises(ValueError):
+        cache.rope_append_hot(0, q.bfloat16(), k, v, cs, cs, 8)    # mixed dtypes
     with pytest.raises(ValueError):
         cache.rope_append_hot(0, q, k, v, cs[..., :32], cs[..., :32], 8)   # cos width
     with pytest.raises(ValueError):

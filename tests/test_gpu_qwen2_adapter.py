@@ -8,7 +8,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _model(gpu, attn="sdpa", layers=2):
+def _model(gpu, attn="sdpa", layers=2, dtype=torch.float16):
     from transformers import Qwen2Config, Qwen2ForCausalLM
     cfg = Qwen2Config(vocab_size=2000, hidden_size=512, intermediate_size=1024,
                       num_hidden_layers=layers, num_attention_heads=8, num_key_value_heads=2,
@@ -18,7 +18,7 @@ def _model(gpu, attn="sdpa", layers=2):
         model = Qwen2ForCausalLM(cfg)
     for p in model.parameters():           # wider weights than the default init, so the
         p.data.normal_(0.0, 0.06)          # logits spread and small errors would show
-    return model.half().eval()
+    return model.to(dtype).eval()
 
 
 def _close(a, b):
@@ -28,12 +28,15 @@ def _close(a, b):
     return cos, rel
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @torch.no_grad()
-def test_decode_and_chunk_match_the_dense_cache(gpu):
+def test_decode_and_chunk_match_the_dense_cache(gpu, dtype):
+    """fp16 and bf16 models (both take the fused RoPE append in decode steps)."""
     from transformers import DynamicCache
     from phasekv_amd.qwen2_attention import (install_qwen2_phasekv_attention, phasekv_prefill,
                                              phasekv_step)
-    model = _model(gpu)
+    print(f"case dtype={dtype}", flush=True)
+    model = _model(gpu, dtype=dtype)
     install_qwen2_phasekv_attention(model)
     g = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, 2000, (1, 300), generator=g).to(gpu)
