@@ -83,6 +83,19 @@ int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_t* shape,
                      uint8_t* out_packed, uint16_t* out_scale, uint16_t* out_mins,
                      int layout, void* stream);
 
+/* The cache's K/V block pack in one launch (_pack_kv, src/phasekv/phasekv_cache.py:101-107:
+ * quantize_pack(K, bits, axis=-2) and quantize_pack(V, bits, axis=-1), groups of
+ * 32).  k, v: fp16 [batch, num_kv_heads, seq_len, head_dim] contiguous, 16-byte
+ * aligned; seq_len and head_dim multiples of 32.  Outputs as pk_quantize_pack
+ * writes them with both layout flags for K: k_packed [B, H, seq_len/vpb,
+ * head_dim], k_scale / k_mins [B, H, seq_len/32, head_dim]; v_packed [B, H,
+ * seq_len, head_dim/vpb], v_scale / v_mins [B, H, seq_len, head_dim/32]; code
+ * buffers 4-byte aligned.  Bit-identical to the two pk_quantize_pack calls. */
+int pk_quantize_pack_kv(const uint16_t* k, const uint16_t* v, int batch, int num_kv_heads,
+                        int64_t seq_len, int head_dim, int bits, uint8_t* k_packed,
+                        uint16_t* k_scale, uint16_t* k_mins, uint8_t* v_packed,
+                        uint16_t* v_scale, uint16_t* v_mins, void* stream);
+
 /* unpack_dequantize (packing.py:158-175): inverse of pk_quantize_pack.  Writes
  * fp16 out contiguous in the ORIGINAL layout orig_shape (ndim <= 8), with
  * n_groups = number of groups per row stored in scale/mins. */

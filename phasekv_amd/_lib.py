@@ -85,6 +85,9 @@ _SIGNATURES = {
                                         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64),
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         _c_vp, _c_vp, _c_vp, ctypes.c_int, _c_vp]),
+    "pk_quantize_pack_kv": (ctypes.c_int, [_c_vp, _c_vp, ctypes.c_int, ctypes.c_int, _c_i64,
+                                           ctypes.c_int, ctypes.c_int, _c_vp, _c_vp, _c_vp, _c_vp,
+                                           _c_vp, _c_vp, _c_vp]),
     "pk_unpack_dequantize": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, ctypes.c_int,
                                             ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int, _c_i64, _c_vp, _c_vp]),

@@ -221,14 +221,16 @@ __device__ __forceinline__ void store_quarter(uint8_t* dst, uint64_t x) {
 
 // Groups along the contiguous axis (V, per token along head_dim): a lane quad
 // per (row, group), the group index fastest; each lane one 16-byte load.
+// `block` / `nblocks`: this workgroup's place in the part of the grid doing this work.
 template <int BITS>
-__global__ void __launch_bounds__(kThreads)
-quantize_inner32_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t len, int64_t ngroups,
-                        int64_t nbytes, uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
-                        uint16_t* __restrict__ mins) {
+__device__ __forceinline__ void inner32_body(const uint16_t* __restrict__ x, int64_t rows,
+                                             int64_t len, int64_t ngroups, int64_t nbytes,
+                                             uint8_t* __restrict__ packed,
+                                             uint16_t* __restrict__ scale,
+                                             uint16_t* __restrict__ mins, int64_t block,
+                                             int64_t nblocks) {
   const int64_t total = rows * ngroups * 4;     // whole quads: every quad runs one iteration
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t i = block * blockDim.x + threadIdx.x; i < total; i += nblocks * blockDim.x) {
     const int quarter = (int)(i & 3);
     const int64_t j = i >> 2;
     const int64_t r = j / ngroups, g = j - r * ngroups;
@@ -248,21 +250,29 @@ quantize_inner32_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t le
   }
 }
 
+template <int BITS>
+__global__ void __launch_bounds__(kThreads)
+quantize_inner32_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t len, int64_t ngroups,
+                        int64_t nbytes, uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
+                        uint16_t* __restrict__ mins) {
+  inner32_body<BITS>(x, rows, len, ngroups, nbytes, packed, scale, mins, blockIdx.x, gridDim.x);
+}
+
 // Groups along the second-innermost axis with a contiguous innermost dim D
 // (K, per channel along tokens): a lane quad per (outer, group, channel pair),
 // quarter fastest, then the channel pair, so each load instruction of a wave
 // reads 64-byte runs of four token rows; each quad stores two channels' packed
 // group and metadata.
 template <int BITS>
-__global__ void __launch_bounds__(kThreads)
-quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t len, int64_t D,
-                        int64_t ngroups, int64_t nbytes, uint8_t* __restrict__ packed,
-                        uint16_t* __restrict__ scale, uint16_t* __restrict__ mins, int meta_gm,
-                        int codes_tm) {
+__device__ __forceinline__ void outer32_body(const uint16_t* __restrict__ x, int64_t outer,
+                                             int64_t len, int64_t D, int64_t ngroups,
+                                             int64_t nbytes, uint8_t* __restrict__ packed,
+                                             uint16_t* __restrict__ scale,
+                                             uint16_t* __restrict__ mins, int meta_gm,
+                                             int codes_tm, int64_t block, int64_t nblocks) {
   const int64_t pairs = D / 2;
   const int64_t total = outer * ngroups * pairs * 4;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t i = block * blockDim.x + threadIdx.x; i < total; i += nblocks * blockDim.x) {
     const int quarter = (int)(i & 3);
     const int64_t rest = i >> 2;
     const int64_t cp = rest % pairs;
@@ -303,6 +313,38 @@ quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t l
       }
     }
   }
+}
+
+template <int BITS>
+__global__ void __launch_bounds__(kThreads)
+quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t len, int64_t D,
+                        int64_t ngroups, int64_t nbytes, uint8_t* __restrict__ packed,
+                        uint16_t* __restrict__ scale, uint16_t* __restrict__ mins, int meta_gm,
+                        int codes_tm) {
+  outer32_body<BITS>(x, outer, len, D, ngroups, nbytes, packed, scale, mins, meta_gm, codes_tm,
+                     blockIdx.x, gridDim.x);
+}
+
+// The cache's K/V block pack in one launch: workgroups [0, k_blocks) pack K
+// [B, H, S, D] per channel along tokens (token-major codes, group-major
+// metadata), the rest pack V per token along head_dim.
+struct KVPackArgs {
+  const uint16_t* k; const uint16_t* v;
+  int64_t outer, S, D;
+  uint8_t* kp; uint16_t* ks; uint16_t* km;
+  uint8_t* vp; uint16_t* vs; uint16_t* vm;
+  int k_blocks;
+};
+
+template <int BITS>
+__global__ void __launch_bounds__(kThreads)
+quantize_kv32_kernel(const KVPackArgs a) {
+  if ((int)blockIdx.x < a.k_blocks)
+    outer32_body<BITS>(a.k, a.outer, a.S, a.D, a.S / 32, a.S * BITS / 8, a.kp, a.ks, a.km, 1, 1,
+                       blockIdx.x, a.k_blocks);
+  else
+    inner32_body<BITS>(a.v, a.outer * a.S, a.D, a.D / 32, a.D * BITS / 8, a.vp, a.vs, a.vm,
+                       blockIdx.x - a.k_blocks, gridDim.x - a.k_blocks);
 }
 
 // General group sizes: metadata per (row, group) ...
@@ -515,6 +557,38 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
                        0, s, p);
   }
   return pk::check_launch("quantize_pack");
+}
+
+extern "C" int pk_quantize_pack_kv(const uint16_t* k, const uint16_t* v, int batch,
+                                   int num_kv_heads, int64_t seq_len, int head_dim, int bits,
+                                   uint8_t* k_packed, uint16_t* k_scale, uint16_t* k_mins,
+                                   uint8_t* v_packed, uint16_t* v_scale, uint16_t* v_mins,
+                                   void* stream) {
+  pk::clear_error();
+  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+  if (!k || !v || !k_packed || !k_scale || !k_mins || !v_packed || !v_scale || !v_mins)
+    return pk::fail("null K / V / output pointer");
+  if (batch <= 0 || num_kv_heads <= 0 || seq_len <= 0 || head_dim <= 0)
+    return pk::fail("batch, num_kv_heads, seq_len and head_dim must be positive");
+  if (seq_len % 32 || head_dim % 32)
+    return pk::fail("the one-launch K/V pack needs seq_len and head_dim multiples of 32");
+  if (reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(v) % 16 ||
+      reinterpret_cast<uintptr_t>(k_packed) % 4 || reinterpret_cast<uintptr_t>(v_packed) % 4)
+    return pk::fail("K / V must be 16-byte aligned and the code buffers 4-byte aligned");
+  KVPackArgs a{k, v, (int64_t)batch * num_kv_heads, seq_len, head_dim, k_packed, k_scale,
+               k_mins, v_packed, v_scale, v_mins, 0};
+  const int64_t k_lanes = a.outer * (seq_len / 32) * (head_dim / 2) * 4;
+  const int64_t v_lanes = a.outer * seq_len * (head_dim / 32) * 4;
+  a.k_blocks = grid_for(k_lanes);
+  const int grid = a.k_blocks + grid_for(v_lanes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (bits == 2)
+    hipLaunchKernelGGL(quantize_kv32_kernel<2>, dim3(grid), dim3(kThreads), 0, s, a);
+  else if (bits == 4)
+    hipLaunchKernelGGL(quantize_kv32_kernel<4>, dim3(grid), dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(quantize_kv32_kernel<8>, dim3(grid), dim3(kThreads), 0, s, a);
+  return pk::check_launch("quantize_pack_kv");
 }
 
 extern "C" int pk_unpack_dequantize(const uint8_t* packed, const uint16_t* scale,

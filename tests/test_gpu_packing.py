@@ -153,3 +153,36 @@ def test_errors_are_value_errors(gpu):
         packing.quantize_pack(x[:, :, :0], 2, -2, 4)
     with pytest.raises(ValueError):
         packing.unpack_low_bits(torch.zeros(4, dtype=torch.int32, device=gpu), 2, 4)
+
+
+@pytest.mark.parametrize("shape,bits", [((1, 4, 8192, 128), 2), ((2, 3, 64, 64), 4),
+                                        ((1, 2, 96, 128), 8), ((3, 1, 32, 32), 2)])
+def test_pack_kv_one_launch_matches_two_quantize_packs(gpu, shape, bits):
+    """``pack_kv``'s one-launch path (``pk_quantize_pack_kv``) gives the tensors, views,
+    fields and bits of ``quantize_pack(K, axis=-2)`` and ``quantize_pack(V, axis=-1)``,
+    with signed zeros, infinities and NaNs among the inputs."""
+    from phasekv_amd.kernels.packing import quantize_pack
+    from phasekv_amd.tiers import _one_launch, pack_kv
+    print(f"case shape={shape} bits={bits}", flush=True)
+    g = torch.Generator().manual_seed(sum(shape) + bits)
+    k = torch.randn(*shape, generator=g) * 3
+    v = torch.randn(*shape, generator=g)
+    flat = k.view(-1)
+    idx = torch.randint(0, flat.numel(), (64,), generator=g)
+    flat[idx[:16]] = 0.0
+    flat[idx[16:32]] = -0.0
+    flat[idx[32:40]] = float("inf")
+    flat[idx[40:44]] = float("nan")
+    v.view(-1)[idx[44:60] % v.numel()] = -0.0
+    k, v = k.to(torch.float16).to(gpu), v.to(torch.float16).to(gpu)
+    assert _one_launch(k, v, bits, 32)
+    got = pack_kv(k, v, bits, 32)
+    want_k, want_v = quantize_pack(k, bits, axis=-2, group_size=32), \
+        quantize_pack(v, bits, axis=-1, group_size=32)
+    for a, b in ((got.key, want_k), (got.value, want_v)):
+        assert (a.bits, a.axis, a.group_size, tuple(a.orig_shape), a.axis_len) == \
+            (b.bits, b.axis, b.group_size, tuple(b.orig_shape), b.axis_len)
+        for x, y in ((a.packed, b.packed), (a.scale, b.scale), (a.mins, b.mins)):
+            assert x.shape == y.shape and x.stride() == y.stride()
+            assert torch.equal(x.contiguous().flatten().view(torch.uint8),
+                               y.contiguous().flatten().view(torch.uint8))
