@@ -8,9 +8,10 @@ cache and attends over the packed tiers with the HIP decode path
 (``qwen2_attention.py:32-109``).  Any other cache goes to the original module.
 
 Differences: transformers 5.x passes ``past_key_values`` and ``position_embeddings``
-and expects ``(output, weights)``; a new input chunk is attended in one pass by
-``fused_phasekv_prompt_chunk_attention`` after its tokens are appended (the reference
-loops token by token, ``:100-106``).  ``phasekv_prefill`` and ``phasekv_step`` drive
+and expects ``(output, weights)``; a new input chunk is appended in one launch and
+attended in one pass by ``fused_phasekv_prompt_chunk_attention`` (the reference loops
+token by token, ``:100-106``); a decode step's RoPE, fp16 casts and window append are
+one launch (``PhaseKVCache.rope_append_hot``, ``:89-92, 77``).  ``phasekv_prefill`` and ``phasekv_step`` drive
 the model the way the reference's usage notes do: prefill with the dense cache and the
 eager attention (for the selection votes), then one step per token, then
 ``finish_decode_step`` / ``finish_prompt_chunk`` after the whole forward pass.
