@@ -298,12 +298,17 @@ extern "C" int pk_prompt_votes(const void* attention, int dtype, int64_t batch, 
   const bool vec = dtype != PK_DTYPE_F32 && strides[3] == 1 && kv_len % 4 == 0 &&
                    strides[0] % 4 == 0 && strides[1] % 4 == 0 && strides[2] % 4 == 0 &&
                    reinterpret_cast<uintptr_t>(attention) % 8 == 0;
-  const int kpl = vec ? 4 : 1;
+  // 2 keys per lane (4-byte loads) when 4 per lane would leave CUs without a workgroup
+  int kpl = vec ? 4 : 1;
+  if (vec && batch * num_kv_heads * pk::cdiv(kv_len, 64 * 4) < pk::device_cu_count()) kpl = 2;
   const int64_t blocks = batch * num_kv_heads * pk::cdiv(kv_len, 64 * kpl);
   if (blocks > 0x7fffffff) return pk::fail("attention too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (vec)
+  if (kpl == 4)
     hipLaunchKernelGGL(votes_kernel<4>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+                       num_kv_heads, G, q_len, kv_len, w, votes);
+  else if (kpl == 2)
+    hipLaunchKernelGGL(votes_kernel<2>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
                        num_kv_heads, G, q_len, kv_len, w, votes);
   else
     hipLaunchKernelGGL(votes_kernel<1>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,

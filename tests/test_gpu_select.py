@@ -33,6 +33,18 @@ def test_votes_bit_exact(gpu, dtype):
     assert np.array_equal(got, so.observation_votes(a[:, :, 30:].float().numpy(), 4, 8))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,hq,hkv,kv", [(2, 16, 8, 4096), (1, 28, 4, 8192), (1, 6, 2, 998)])
+def test_votes_bit_exact_per_load_width(gpu, dtype, B, hq, hkv, kv):
+    """16-bit attention takes 4 keys per lane when that gives every CU a workgroup
+    (2 x 8 kv heads x 4096 keys), else 2 (C4's 4 kv heads x 8192) or 1 (rows of 998 keys)."""
+    from phasekv_amd.prompt_tier import prompt_votes
+    print(f"case B={B} hq={hq} hkv={hkv} kv={kv} {dtype}", flush=True)
+    a = _attn(B + kv, B, hq, 24, kv).to(dtype)
+    got = prompt_votes(a.to(gpu), hkv, 24).cpu().numpy()
+    assert np.array_equal(got, so.observation_votes(a.float().numpy(), hkv, 24))
+
+
 @pytest.mark.parametrize("pooling,kernel", [("maxpool", 7), ("avgpool", 7), ("maxpool", 4),
                                             ("avgpool", 2), ("maxpool", 1)])
 @pytest.mark.parametrize("L,ratio,sink,obs", [(300, 0.3, 4, 32), (2048, 0.1, 4, 64),
