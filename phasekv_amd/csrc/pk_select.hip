@@ -17,7 +17,8 @@
 
 namespace {
 
-constexpr int kSelThreads = 256;
+constexpr int kSelThreads = 256;     // votes kernel
+constexpr int kPickThreads = 1024;   // selection kernel: 16 waves share one row's candidates
 // candidates whose votes and keys are staged in LDS (8 bytes each, 144 KB)
 constexpr int64_t kMaxStagedKeys = 18 * 1024;
 
@@ -138,7 +139,7 @@ __device__ __forceinline__ uint32_t score_key(float v) {
 }
 
 // Exclusive prefix sum of v over the workgroup's threads (tid order); uses
-// scratch[kSelThreads / 64] and synchronizes the workgroup.
+// scratch[waves of the workgroup] and synchronizes the workgroup.
 __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* scratch) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int64_t inc = v;
@@ -169,42 +170,42 @@ struct KeySource {
 // One workgroup per (b, kv): sink positions, then the select_k best pooled
 // candidates of [sink, recent_start) (ties: the earlier position), then the
 // recent positions, in ascending order.
-__global__ void __launch_bounds__(kSelThreads)
+__global__ void __launch_bounds__(kPickThreads)
 select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int64_t recent_start,
               int64_t select_k, int pool_k, int pool_mode, int64_t* __restrict__ keep,
               int64_t budget, int staged) {
   extern __shared__ uint32_t lds_keys[];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_prefix, s_mask, s_need;
-  __shared__ int64_t s_count[kSelThreads / 64];
+  __shared__ int64_t s_count[kPickThreads / 64];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const float* c = votes + row * kv_len + sink;
   const int64_t n = recent_start - sink;
   int64_t* out = keep + row * budget;
-  for (int64_t i = tid; i < sink; i += kSelThreads) out[i] = i;
-  for (int64_t i = tid; i < kv_len - recent_start; i += kSelThreads)
+  for (int64_t i = tid; i < sink; i += kPickThreads) out[i] = i;
+  for (int64_t i = tid; i < kv_len - recent_start; i += kPickThreads)
     out[sink + select_k + i] = recent_start + i;
   if (select_k <= 0) return;
   KeySource key_of{c, n, pool_k, pool_mode, nullptr};
   if (staged) {
     // the row's votes into LDS (8 loads in flight per thread), then the keys
     float* raw = reinterpret_cast<float*>(lds_keys + n);
-    for (int64_t j0 = tid; j0 < n; j0 += 8 * kSelThreads) {
+    for (int64_t j0 = tid; j0 < n; j0 += 8 * kPickThreads) {
       float x[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int64_t j = j0 + u * kSelThreads;
+        const int64_t j = j0 + u * kPickThreads;
         x[u] = j < n ? c[j] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int64_t j = j0 + u * kSelThreads;
+        const int64_t j = j0 + u * kPickThreads;
         if (j < n) raw[j] = x[u];
       }
     }
     __syncthreads();
-    for (int64_t j = tid; j < n; j += kSelThreads)
+    for (int64_t j = tid; j < n; j += kPickThreads)
       lds_keys[j] = score_key(pooled(raw, n, j, pool_k, pool_mode));
     key_of.lds = lds_keys;
   }
@@ -216,31 +217,34 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
   }
   __syncthreads();
   for (int shift = 24; shift >= 0; shift -= 8) {
-    hist[tid] = 0;
+    if (tid < 256) hist[tid] = 0;
     __syncthreads();
     const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int64_t j = tid; j < n; j += kSelThreads) {
+    for (int64_t j = tid; j < n; j += kPickThreads) {
       const uint32_t key = key_of(j);
       if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
     }
     __syncthreads();
     // suffix sums of the histogram (thread t: keys with digit >= t), then the one
     // digit d with suffix(d) >= need > suffix(d + 1) is the threshold's digit
+    // (threads 0..255, the first four waves, own one digit each)
     const uint32_t need = s_need;
-    uint32_t suf = hist[tid];
+    const bool digit = tid < 256;
+    uint32_t suf = digit ? hist[tid] : 0u;
     for (int o = 1; o < 64; o <<= 1) {
       const uint32_t v = __shfl_down(suf, o);
       if ((tid & 63) + o < 64) suf += v;
     }
     __syncthreads();
-    hist[tid] = suf;                       // suffix within the wave
+    if (digit) hist[tid] = suf;            // suffix within the wave
     __syncthreads();
-    for (int wv = (tid >> 6) + 1; wv < kSelThreads / 64; ++wv) suf += hist[wv * 64];
+    if (digit)
+      for (int wv = (tid >> 6) + 1; wv < 4; ++wv) suf += hist[wv * 64];
     __syncthreads();
-    hist[tid] = suf;                       // full suffix sums
+    if (digit) hist[tid] = suf;            // full suffix sums
     __syncthreads();
     const uint32_t next = tid < 255 ? hist[tid + 1] : 0u;
-    if (suf >= need && next < need) {
+    if (digit && suf >= need && next < need) {
       s_prefix = prefix | ((uint32_t)tid << shift);
       s_mask = mask | (255u << shift);
       s_need = need - next;
@@ -252,7 +256,7 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
   const int64_t take_equal = s_need;
   // each thread scans one contiguous range: counts, then a block scan of the
   // counts gives each thread its first output slot
-  const int64_t per = (n + kSelThreads - 1) / kSelThreads;
+  const int64_t per = (n + kPickThreads - 1) / kPickThreads;
   const int64_t j0 = min<int64_t>(n, tid * per), j1 = min<int64_t>(n, j0 + per);
   int64_t above = 0, equal = 0;
   for (int64_t j = j0; j < j1; ++j) {
@@ -338,7 +342,7 @@ extern "C" int pk_select_prompt(const float* votes, int64_t rows, int64_t kv_len
   }();
   if (staged && lds > 64 * 1024 && !lds_opt_in)
     return pk::fail("cannot reserve the selection kernel's LDS"), PK_ERR_RUNTIME;
-  hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(kSelThreads), lds,
+  hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(kPickThreads), lds,
                      static_cast<hipStream_t>(stream), votes, kv_len, sink, recent_start,
                      select_k, pool_kernel, pool_mode, keep, budget, staged);
   return pk::check_launch("select_prompt");
