@@ -123,12 +123,15 @@ def partial_from_dense(q: np.ndarray, k: np.ndarray, v: np.ndarray, num_attentio
     """(m, l, acc) of q [Hq, hd] against one segment's dense K/V [Hkv, S, hd]."""
     hkv, s_len, hd = k.shape
     group = num_attention_heads // hkv
-    kk = np.repeat(k.astype(dtype), group, axis=0)
-    vv = np.repeat(v.astype(dtype), group, axis=0)
-    s = np.einsum("hd,hsd->hs", q.astype(dtype), kk) * dtype(1.0 / math.sqrt(hd))
+    # query head h reads kv head h // group (reference.py:61-69); the heads of one kv
+    # head are a batch of one matrix product instead of a repeated K/V copy
+    qg = q.astype(dtype).reshape(hkv, group, hd)
+    s = np.matmul(qg, np.swapaxes(k.astype(dtype), 1, 2)) * dtype(1.0 / math.sqrt(hd))
+    s = s.reshape(num_attention_heads, s_len)
     m = s.max(axis=1)
     p = np.exp(s - m[:, None])
-    return m, p.sum(axis=1), np.einsum("hs,hsd->hd", p, vv)
+    acc = np.matmul(p.reshape(hkv, group, s_len), v.astype(dtype)).reshape(num_attention_heads, hd)
+    return m, p.sum(axis=1), acc
 
 
 def split_partials(q, k, v, num_attention_heads, split_len, dtype=np.float64):

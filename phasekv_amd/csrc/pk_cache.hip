@@ -463,20 +463,22 @@ extern "C" int pk_append_hot(const uint16_t* k_src, const uint16_t* v_src, int64
                              int64_t hot_hstride, int64_t hot_tstride, int batch,
                              int num_kv_heads, int head_dim, int64_t position, int64_t capacity,
                              void* stream) {
-  pk::clear_error();
-  if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
-                         hot_tstride))
-    return rc;
-  if (!k_src || !v_src) return pk::fail("null K/V source");
-  if (position < 0 || position >= capacity) return pk::fail("hot window is full");
-  const int64_t total = (int64_t)batch * num_kv_heads * head_dim;
-  const int grid = (int)std::min<int64_t>(pk::cdiv(total, kCoolThreads), 4096);
-  hipLaunchKernelGGL(append_hot_kernel, dim3(grid), dim3(kCoolThreads), 0,
-                     static_cast<hipStream_t>(stream), k_src, v_src,
-                     SrcView{k_bstride, k_hstride, 0}, SrcView{v_bstride, v_hstride, 0}, hot_k,
-                     hot_v, HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads,
-                     head_dim, position, (int64_t)1, total);
-  return pk::check_launch("append_hot");
+  return pk::guarded("pk_append_hot", [&]() -> int {
+    pk::clear_error();
+    if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
+                           hot_tstride))
+      return rc;
+    if (!k_src || !v_src) return pk::fail("null K/V source");
+    if (position < 0 || position >= capacity) return pk::fail("hot window is full");
+    const int64_t total = (int64_t)batch * num_kv_heads * head_dim;
+    const int grid = (int)std::min<int64_t>(pk::cdiv(total, kCoolThreads), 4096);
+    hipLaunchKernelGGL(append_hot_kernel, dim3(grid), dim3(kCoolThreads), 0,
+                       static_cast<hipStream_t>(stream), k_src, v_src,
+                       SrcView{k_bstride, k_hstride, 0}, SrcView{v_bstride, v_hstride, 0}, hot_k,
+                       hot_v, HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads,
+                       head_dim, position, (int64_t)1, total);
+    return pk::check_launch("append_hot");
+  });
 }
 
 extern "C" int pk_append_hot_rows(const uint16_t* k_src, const uint16_t* v_src, int64_t k_bstride,
@@ -486,23 +488,25 @@ extern "C" int pk_append_hot_rows(const uint16_t* k_src, const uint16_t* v_src, 
                                   int64_t hot_tstride, int batch, int num_kv_heads, int head_dim,
                                   int64_t position, int64_t count, int64_t capacity,
                                   void* stream) {
-  pk::clear_error();
-  if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
-                         hot_tstride))
-    return rc;
-  if (!k_src || !v_src) return pk::fail("null K/V source");
-  if (count <= 0) return pk::fail("count must be positive");
-  if (position < 0 || position > capacity - count)
-    return pk::fail("the rows do not fit in the hot window");
-  const int64_t total = (int64_t)batch * num_kv_heads * count * head_dim;
-  const int grid = (int)std::min<int64_t>(pk::cdiv(total, kCoolThreads), 4096);
-  hipLaunchKernelGGL(append_hot_kernel, dim3(grid), dim3(kCoolThreads), 0,
-                     static_cast<hipStream_t>(stream), k_src, v_src,
-                     SrcView{k_bstride, k_hstride, k_tstride},
-                     SrcView{v_bstride, v_hstride, v_tstride}, hot_k, hot_v,
-                     HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
-                     position, count, total);
-  return pk::check_launch("append_hot_rows");
+  return pk::guarded("pk_append_hot_rows", [&]() -> int {
+    pk::clear_error();
+    if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
+                           hot_tstride))
+      return rc;
+    if (!k_src || !v_src) return pk::fail("null K/V source");
+    if (count <= 0) return pk::fail("count must be positive");
+    if (position < 0 || position > capacity - count)
+      return pk::fail("the rows do not fit in the hot window");
+    const int64_t total = (int64_t)batch * num_kv_heads * count * head_dim;
+    const int grid = (int)std::min<int64_t>(pk::cdiv(total, kCoolThreads), 4096);
+    hipLaunchKernelGGL(append_hot_kernel, dim3(grid), dim3(kCoolThreads), 0,
+                       static_cast<hipStream_t>(stream), k_src, v_src,
+                       SrcView{k_bstride, k_hstride, k_tstride},
+                       SrcView{v_bstride, v_hstride, v_tstride}, hot_k, hot_v,
+                       HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
+                       position, count, total);
+    return pk::check_launch("append_hot_rows");
+  });
 }
 
 extern "C" int pk_rope_append_hot(const uint16_t* q, int64_t q_bstride, const uint16_t* k,
@@ -513,77 +517,83 @@ extern "C" int pk_rope_append_hot(const uint16_t* q, int64_t q_bstride, const ui
                                   int64_t hot_hstride, int64_t hot_tstride, int batch,
                                   int num_q_heads, int num_kv_heads, int head_dim,
                                   int64_t position, int64_t capacity, void* stream) {
-  pk::clear_error();
-  if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
-                         hot_tstride))
-    return rc;
-  if (!q || !k || !v || !cos || !sin || !q_out) return pk::fail("null q / K / V / cos / sin / q_out");
-  if (num_q_heads <= 0 || num_q_heads % num_kv_heads)
-    return pk::fail("num_q_heads must be a positive multiple of num_kv_heads");
-  if (head_dim % 2) return pk::fail("head_dim must be even for the rotary embedding");
-  if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16)
-    return pk::fail("q / K / V / cos / sin must be float16 or bfloat16");
-  if (q_bstride < (int64_t)num_q_heads * head_dim || kv_bstride < (int64_t)num_kv_heads * head_dim ||
-      cs_bstride < 0)
-    return pk::fail("q / K / V batch strides must cover their heads; cos / sin stride >= 0");
-  if (position < 0 || position >= capacity) return pk::fail("hot window is full");
-  const int64_t total = (int64_t)batch * (num_q_heads + num_kv_heads) * (head_dim / 2);
-  const int grid = (int)std::min<int64_t>(pk::cdiv(total, 256), 4096);
-  if (dtype == PK_DTYPE_BF16)
-    hipLaunchKernelGGL(rope_append_kernel<true>, dim3(grid), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), q, q_bstride, k, v, kv_bstride, cos, sin,
-                       cs_bstride, q_out, hot_k, hot_v,
-                       HotView{hot_bstride, hot_hstride, hot_tstride}, num_q_heads, num_kv_heads,
-                       head_dim, position, total);
-  else
-    hipLaunchKernelGGL(rope_append_kernel<false>, dim3(grid), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), q, q_bstride, k, v, kv_bstride, cos, sin,
-                       cs_bstride, q_out, hot_k, hot_v,
-                       HotView{hot_bstride, hot_hstride, hot_tstride}, num_q_heads, num_kv_heads,
-                       head_dim, position, total);
-  return pk::check_launch("rope_append_hot");
+  return pk::guarded("pk_rope_append_hot", [&]() -> int {
+    pk::clear_error();
+    if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
+                           hot_tstride))
+      return rc;
+    if (!q || !k || !v || !cos || !sin || !q_out) return pk::fail("null q / K / V / cos / sin / q_out");
+    if (num_q_heads <= 0 || num_q_heads % num_kv_heads)
+      return pk::fail("num_q_heads must be a positive multiple of num_kv_heads");
+    if (head_dim % 2) return pk::fail("head_dim must be even for the rotary embedding");
+    if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16)
+      return pk::fail("q / K / V / cos / sin must be float16 or bfloat16");
+    if (q_bstride < (int64_t)num_q_heads * head_dim || kv_bstride < (int64_t)num_kv_heads * head_dim ||
+        cs_bstride < 0)
+      return pk::fail("q / K / V batch strides must cover their heads; cos / sin stride >= 0");
+    if (position < 0 || position >= capacity) return pk::fail("hot window is full");
+    const int64_t total = (int64_t)batch * (num_q_heads + num_kv_heads) * (head_dim / 2);
+    const int grid = (int)std::min<int64_t>(pk::cdiv(total, 256), 4096);
+    if (dtype == PK_DTYPE_BF16)
+      hipLaunchKernelGGL(rope_append_kernel<true>, dim3(grid), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), q, q_bstride, k, v, kv_bstride, cos, sin,
+                         cs_bstride, q_out, hot_k, hot_v,
+                         HotView{hot_bstride, hot_hstride, hot_tstride}, num_q_heads, num_kv_heads,
+                         head_dim, position, total);
+    else
+      hipLaunchKernelGGL(rope_append_kernel<false>, dim3(grid), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), q, q_bstride, k, v, kv_bstride, cos, sin,
+                         cs_bstride, q_out, hot_k, hot_v,
+                         HotView{hot_bstride, hot_hstride, hot_tstride}, num_q_heads, num_kv_heads,
+                         head_dim, position, total);
+    return pk::check_launch("rope_append_hot");
+  });
 }
 
 extern "C" int pk_cool_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride,
                            int64_t hot_hstride, int64_t hot_tstride, int batch, int num_kv_heads,
                            int head_dim, int64_t hot_len, int64_t aged, int64_t keep,
                            uint16_t* out_k, uint16_t* out_v, int64_t* out_index, void* stream) {
-  pk::clear_error();
-  if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
-                         hot_tstride))
-    return rc;
-  if (aged <= 0 || aged > hot_len) return pk::fail("aged must be in [1, hot_len]");
-  if (aged > PK_COOL_MAX_AGED) return pk::fail("aged above PK_COOL_MAX_AGED");
-  if (keep <= 0 || keep > aged) return pk::fail("keep must be in [1, aged]");
-  if (!out_k || !out_v) return pk::fail("null output buffer");
-  const size_t meta = (size_t)aged * (sizeof(float) + 2 * sizeof(int));
-  const size_t staged = staged_lds(hot_len, head_dim, aged, keep, false, 0, 0);
-  const bool vec = hot_vectors(hot_k, hot_v, head_dim, hot_bstride, hot_hstride, hot_tstride) &&
-                   reinterpret_cast<uintptr_t>(out_k) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(out_v) % 16 == 0;
-  if (vec && staged) {
-    hipLaunchKernelGGL(cool_hot_staged_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads),
-                       staged, static_cast<hipStream_t>(stream), hot_k, hot_v,
+  return pk::guarded("pk_cool_hot", [&]() -> int {
+    pk::clear_error();
+    if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
+                           hot_tstride))
+      return rc;
+    if (aged <= 0 || aged > hot_len) return pk::fail("aged must be in [1, hot_len]");
+    if (aged > PK_COOL_MAX_AGED) return pk::fail("aged above PK_COOL_MAX_AGED");
+    if (keep <= 0 || keep > aged) return pk::fail("keep must be in [1, aged]");
+    if (!out_k || !out_v) return pk::fail("null output buffer");
+    const size_t meta = (size_t)aged * (sizeof(float) + 2 * sizeof(int));
+    const size_t staged = staged_lds(hot_len, head_dim, aged, keep, false, 0, 0);
+    const bool vec = hot_vectors(hot_k, hot_v, head_dim, hot_bstride, hot_hstride, hot_tstride) &&
+                     reinterpret_cast<uintptr_t>(out_k) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(out_v) % 16 == 0;
+    if (vec && staged) {
+      hipLaunchKernelGGL(cool_hot_staged_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads),
+                         staged, static_cast<hipStream_t>(stream), hot_k, hot_v,
+                         HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
+                         (int)hot_len, (int)aged, (int)keep, out_k, out_v, out_index);
+      return pk::check_launch("cool_hot");
+    }
+    const size_t lds = meta;
+    hipLaunchKernelGGL(cool_hot_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads), lds,
+                       static_cast<hipStream_t>(stream), hot_k, hot_v,
                        HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
                        (int)hot_len, (int)aged, (int)keep, out_k, out_v, out_index);
     return pk::check_launch("cool_hot");
-  }
-  const size_t lds = meta;
-  hipLaunchKernelGGL(cool_hot_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads), lds,
-                     static_cast<hipStream_t>(stream), hot_k, hot_v,
-                     HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
-                     (int)hot_len, (int)aged, (int)keep, out_k, out_v, out_index);
-  return pk::check_launch("cool_hot");
+  });
 }
 
 extern "C" int pk_cool_pack_supported(int64_t hot_len, int head_dim, int64_t aged, int64_t keep,
                                       int group_size) {
-  if (hot_len <= 0 || head_dim <= 0 || aged <= 0 || aged > hot_len || keep <= 0 || keep > aged ||
-      group_size <= 0)
-    return 0;
-  const int64_t ngk = pk::cdiv(keep, std::min<int64_t>(group_size, keep));
-  const int64_t ngv = pk::cdiv(head_dim, std::min<int64_t>(group_size, head_dim));
-  return staged_lds(hot_len, head_dim, aged, keep, true, ngk, ngv) ? 1 : 0;
+  return pk::guarded("pk_cool_pack_supported", [&]() -> int {
+    if (hot_len <= 0 || head_dim <= 0 || aged <= 0 || aged > hot_len || keep <= 0 || keep > aged ||
+        group_size <= 0)
+      return 0;
+    const int64_t ngk = pk::cdiv(keep, std::min<int64_t>(group_size, keep));
+    const int64_t ngv = pk::cdiv(head_dim, std::min<int64_t>(group_size, head_dim));
+    return staged_lds(hot_len, head_dim, aged, keep, true, ngk, ngv) ? 1 : 0;
+  });
 }
 
 extern "C" int pk_cool_pack_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bstride,
@@ -593,35 +603,37 @@ extern "C" int pk_cool_pack_hot(uint16_t* hot_k, uint16_t* hot_v, int64_t hot_bs
                                 uint16_t* k_scale, uint16_t* k_mins, uint8_t* v_packed,
                                 uint16_t* v_scale, uint16_t* v_mins, int64_t* out_index,
                                 void* stream) {
-  pk::clear_error();
-  if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
-                         hot_tstride))
-    return rc;
-  if (aged <= 0 || aged > hot_len) return pk::fail("aged must be in [1, hot_len]");
-  if (keep <= 0 || keep > aged) return pk::fail("keep must be in [1, aged]");
-  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
-  if (group_size <= 0) return pk::fail("group_size must be positive");
-  if (!k_packed || !k_scale || !k_mins || !v_packed || !v_scale || !v_mins)
-    return pk::fail("null output buffer");
-  if (!pk_cool_pack_supported(hot_len, head_dim, aged, keep, group_size) ||
-      !hot_vectors(hot_k, hot_v, head_dim, hot_bstride, hot_hstride, hot_tstride))
-    return pk::fail("this window does not fit the fused cooling step "
-                    "(use pk_cool_hot and pk_quantize_pack)");
-  PackOut po;
-  po.kp = k_packed; po.ks = k_scale; po.km = k_mins;
-  po.vp = v_packed; po.vs = v_scale; po.vm = v_mins;
-  po.bits = bits;
-  const int vpb = 8 / bits;
-  po.gsk = (int)std::min<int64_t>(group_size, keep);
-  po.ngk = (int)pk::cdiv(keep, po.gsk);
-  po.nbk = (int)pk::cdiv(keep, vpb);
-  po.gsv = std::min(group_size, head_dim);
-  po.ngv = (int)pk::cdiv(head_dim, po.gsv);
-  po.nbv = (int)pk::cdiv(head_dim, vpb);
-  const size_t lds = staged_lds(hot_len, head_dim, aged, keep, true, po.ngk, po.ngv);
-  hipLaunchKernelGGL(cool_pack_staged_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads),
-                     lds, static_cast<hipStream_t>(stream), hot_k, hot_v,
-                     HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
-                     (int)hot_len, (int)aged, (int)keep, po, out_index);
-  return pk::check_launch("cool_pack_hot");
+  return pk::guarded("pk_cool_pack_hot", [&]() -> int {
+    pk::clear_error();
+    if (int rc = check_hot(hot_k, hot_v, batch, num_kv_heads, head_dim, hot_bstride, hot_hstride,
+                           hot_tstride))
+      return rc;
+    if (aged <= 0 || aged > hot_len) return pk::fail("aged must be in [1, hot_len]");
+    if (keep <= 0 || keep > aged) return pk::fail("keep must be in [1, aged]");
+    if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+    if (group_size <= 0) return pk::fail("group_size must be positive");
+    if (!k_packed || !k_scale || !k_mins || !v_packed || !v_scale || !v_mins)
+      return pk::fail("null output buffer");
+    if (!pk_cool_pack_supported(hot_len, head_dim, aged, keep, group_size) ||
+        !hot_vectors(hot_k, hot_v, head_dim, hot_bstride, hot_hstride, hot_tstride))
+      return pk::fail("this window does not fit the fused cooling step "
+                      "(use pk_cool_hot and pk_quantize_pack)");
+    PackOut po;
+    po.kp = k_packed; po.ks = k_scale; po.km = k_mins;
+    po.vp = v_packed; po.vs = v_scale; po.vm = v_mins;
+    po.bits = bits;
+    const int vpb = 8 / bits;
+    po.gsk = (int)std::min<int64_t>(group_size, keep);
+    po.ngk = (int)pk::cdiv(keep, po.gsk);
+    po.nbk = (int)pk::cdiv(keep, vpb);
+    po.gsv = std::min(group_size, head_dim);
+    po.ngv = (int)pk::cdiv(head_dim, po.gsv);
+    po.nbv = (int)pk::cdiv(head_dim, vpb);
+    const size_t lds = staged_lds(hot_len, head_dim, aged, keep, true, po.ngk, po.ngv);
+    hipLaunchKernelGGL(cool_pack_staged_kernel, dim3(batch * num_kv_heads), dim3(kCoolThreads),
+                       lds, static_cast<hipStream_t>(stream), hot_k, hot_v,
+                       HotView{hot_bstride, hot_hstride, hot_tstride}, num_kv_heads, head_dim,
+                       (int)hot_len, (int)aged, (int)keep, po, out_index);
+    return pk::check_launch("cool_pack_hot");
+  });
 }

@@ -5,15 +5,33 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <new>
 #include <string>
 
 #include "phasekv_hip.h"
 
 namespace pk {
 
-// Thread-local error message behind pk_last_error().
+// Thread-local error message behind pk_last_error(): a fixed buffer, so that
+// recording an error never allocates or throws (longer messages are cut).
 void set_error(const std::string& msg);
-void clear_error();
+void set_error_text(const char* a, const char* b) noexcept;
+void clear_error() noexcept;
+
+// Body of every extern "C" entry point: no C++ exception crosses the ABI.  A
+// failed host allocation or any other exception becomes PK_ERR_RUNTIME with a
+// message naming the entry point.
+template <class F>
+inline int guarded(const char* what, F&& body) noexcept {
+  try {
+    return body();
+  } catch (const std::bad_alloc&) {
+    set_error_text(what, ": out of host memory");
+  } catch (...) {
+    set_error_text(what, ": unexpected C++ exception");
+  }
+  return PK_ERR_RUNTIME;
+}
 
 inline int fail(const std::string& msg) {
   set_error(msg);

@@ -645,23 +645,27 @@ using namespace pk;
 
 extern "C" int pk_decode_workspace_size(const pk_decode_problem* p, size_t* bytes,
                                         int32_t* total_splits) {
-  clear_error();
-  int rc = validate_problem(p);
-  if (rc) return rc;
-  Plan pl = make_plan(p);
-  if (bytes) *bytes = pl.bytes;
-  if (total_splits) *total_splits = pl.C;
-  return PK_OK;
+  return pk::guarded("pk_decode_workspace_size", [&]() -> int {
+    clear_error();
+    int rc = validate_problem(p);
+    if (rc) return rc;
+    Plan pl = make_plan(p);
+    if (bytes) *bytes = pl.bytes;
+    if (total_splits) *total_splits = pl.C;
+    return PK_OK;
+  });
 }
 
 extern "C" int pk_decode_partials(const pk_decode_problem* p, void* workspace,
                                   size_t workspace_bytes, void* stream) {
-  clear_error();
-  int rc = validate_problem(p);
-  if (rc) return rc;
-  Plan pl = make_plan(p);
-  if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
-  return launch_partials(p, pl, static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+  return pk::guarded("pk_decode_partials", [&]() -> int {
+    clear_error();
+    int rc = validate_problem(p);
+    if (rc) return rc;
+    Plan pl = make_plan(p);
+    if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
+    return launch_partials(p, pl, static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+  });
 }
 
 static int launch_combine(const float* m, const float* l, const float* acc, int64_t rows, int C,
@@ -682,48 +686,54 @@ static int launch_combine(const float* m, const float* l, const float* acc, int6
 extern "C" int pk_decode_combine(const pk_decode_problem* p, const void* workspace,
                                  uint16_t* out, float* out_m, float* out_l, float* out_acc,
                                  void* stream) {
-  clear_error();
-  int rc = validate_problem(p);
-  if (rc) return rc;
-  if (!workspace) return fail("null workspace");
-  if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
-  Plan pl = make_plan(p);
-  const char* ws = static_cast<const char*>(workspace);
-  return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
-                        reinterpret_cast<const float*>(ws + pl.off_l),
-                        reinterpret_cast<const float*>(ws + pl.off_acc),
-                        (int64_t)p->batch * p->num_q_heads, pl.C, p->head_dim, out, out_m, out_l,
-                        out_acc, static_cast<hipStream_t>(stream), "decode_combine");
+  return pk::guarded("pk_decode_combine", [&]() -> int {
+    clear_error();
+    int rc = validate_problem(p);
+    if (rc) return rc;
+    if (!workspace) return fail("null workspace");
+    if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
+    Plan pl = make_plan(p);
+    const char* ws = static_cast<const char*>(workspace);
+    return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
+                          reinterpret_cast<const float*>(ws + pl.off_l),
+                          reinterpret_cast<const float*>(ws + pl.off_acc),
+                          (int64_t)p->batch * p->num_q_heads, pl.C, p->head_dim, out, out_m, out_l,
+                          out_acc, static_cast<hipStream_t>(stream), "decode_combine");
+  });
 }
 
 extern "C" int pk_fused_decode(const pk_decode_problem* p, void* workspace, size_t workspace_bytes,
                                uint16_t* out, void* stream) {
-  clear_error();
-  int rc = validate_problem(p);
-  if (rc) return rc;
-  if (!out) return fail("null output");
-  Plan pl = make_plan(p);
-  if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  rc = launch_partials(p, pl, static_cast<char*>(workspace), s);
-  if (rc) return rc;
-  const char* ws = static_cast<const char*>(workspace);
-  return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
-                        reinterpret_cast<const float*>(ws + pl.off_l),
-                        reinterpret_cast<const float*>(ws + pl.off_acc),
-                        (int64_t)p->batch * p->num_q_heads, pl.C, p->head_dim, out, nullptr,
-                        nullptr, nullptr, s, "fused_decode");
+  return pk::guarded("pk_fused_decode", [&]() -> int {
+    clear_error();
+    int rc = validate_problem(p);
+    if (rc) return rc;
+    if (!out) return fail("null output");
+    Plan pl = make_plan(p);
+    if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = launch_partials(p, pl, static_cast<char*>(workspace), s);
+    if (rc) return rc;
+    const char* ws = static_cast<const char*>(workspace);
+    return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
+                          reinterpret_cast<const float*>(ws + pl.off_l),
+                          reinterpret_cast<const float*>(ws + pl.off_acc),
+                          (int64_t)p->batch * p->num_q_heads, pl.C, p->head_dim, out, nullptr,
+                          nullptr, nullptr, s, "fused_decode");
+  });
 }
 
 extern "C" int pk_merge_partials(const float* m, const float* l, const float* acc, int64_t rows,
                                  int32_t n, int32_t head_dim, uint16_t* out, float* out_m,
                                  float* out_l, float* out_acc, void* stream) {
-  clear_error();
-  if (rows < 0 || n <= 0 || head_dim <= 0) return fail("rows, n and head_dim must be positive");
-  if (head_dim > kCombineMaxHd || (head_dim & (head_dim - 1)))
-    return fail("head_dim must be a power of two <= 256");
-  if (!m || !l || !acc) return fail("null partials");
-  if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
-  return launch_combine(m, l, acc, rows, n, head_dim, out, out_m, out_l, out_acc,
-                        static_cast<hipStream_t>(stream), "merge_partials");
+  return pk::guarded("pk_merge_partials", [&]() -> int {
+    clear_error();
+    if (rows < 0 || n <= 0 || head_dim <= 0) return fail("rows, n and head_dim must be positive");
+    if (head_dim > kCombineMaxHd || (head_dim & (head_dim - 1)))
+      return fail("head_dim must be a power of two <= 256");
+    if (!m || !l || !acc) return fail("null partials");
+    if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
+    return launch_combine(m, l, acc, rows, n, head_dim, out, out_m, out_l, out_acc,
+                          static_cast<hipStream_t>(stream), "merge_partials");
+  });
 }

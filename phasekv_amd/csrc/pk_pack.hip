@@ -439,124 +439,130 @@ inline int grid_for(int64_t total) {
 // ---------------------------------------------------------------------------
 extern "C" int pk_pack_low_bits(const uint8_t* codes, int64_t rows, int64_t length, int bits,
                                 uint8_t* out, void* stream) {
-  pk::clear_error();
-  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
-  if (rows < 0 || length < 0) return pk::fail("rows and length must be non-negative");
-  const int64_t nbytes = pk::cdiv(length, 8 / bits);
-  if (rows * nbytes == 0) return PK_OK;
-  if (!codes || !out) return pk::fail("null pointer");
-  hipLaunchKernelGGL(pack_low_bits_kernel, dim3(grid_for(rows * nbytes)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), codes, rows, length, bits, nbytes, out);
-  return pk::check_launch("pack_low_bits");
+  return pk::guarded("pk_pack_low_bits", [&]() -> int {
+    pk::clear_error();
+    if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+    if (rows < 0 || length < 0) return pk::fail("rows and length must be non-negative");
+    const int64_t nbytes = pk::cdiv(length, 8 / bits);
+    if (rows * nbytes == 0) return PK_OK;
+    if (!codes || !out) return pk::fail("null pointer");
+    hipLaunchKernelGGL(pack_low_bits_kernel, dim3(grid_for(rows * nbytes)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), codes, rows, length, bits, nbytes, out);
+    return pk::check_launch("pack_low_bits");
+  });
 }
 
 extern "C" int pk_unpack_low_bits(const uint8_t* packed, int64_t rows, int64_t packed_len,
                                   int bits, int64_t length, uint8_t* out, void* stream) {
-  pk::clear_error();
-  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
-  if (rows < 0 || length < 0 || packed_len < 0) return pk::fail("sizes must be non-negative");
-  if (length > packed_len * (8 / bits)) return pk::fail("length exceeds the packed codes");
-  if (rows * length == 0) return PK_OK;
-  if (!packed || !out) return pk::fail("null pointer");
-  hipLaunchKernelGGL(unpack_low_bits_kernel, dim3(grid_for(rows * length)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), packed, rows, packed_len, bits, length, out);
-  return pk::check_launch("unpack_low_bits");
+  return pk::guarded("pk_unpack_low_bits", [&]() -> int {
+    pk::clear_error();
+    if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+    if (rows < 0 || length < 0 || packed_len < 0) return pk::fail("sizes must be non-negative");
+    if (length > packed_len * (8 / bits)) return pk::fail("length exceeds the packed codes");
+    if (rows * length == 0) return PK_OK;
+    if (!packed || !out) return pk::fail("null pointer");
+    hipLaunchKernelGGL(unpack_low_bits_kernel, dim3(grid_for(rows * length)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), packed, rows, packed_len, bits, length, out);
+    return pk::check_launch("unpack_low_bits");
+  });
 }
 
 extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_t* shape,
                                 const int64_t* strides, int axis, int bits, int group_size,
                                 uint8_t* out_packed, uint16_t* out_scale, uint16_t* out_mins,
                                 int layout, void* stream) {
-  pk::clear_error();
-  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
-  if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16 && dtype != PK_DTYPE_F32)
-    return pk::fail("x must be float16, bfloat16 or float32");
-  if (ndim < 1 || ndim > kMaxDims) return pk::fail("x must have 1..8 dims");
-  if (axis < 0 || axis >= ndim) return pk::fail("axis out of range");
-  if (layout & ~(PK_LAYOUT_META_TRANSPOSED | PK_LAYOUT_CODES_TRANSPOSED))
-    return pk::fail("unknown layout flags");
-  if (layout && (ndim < 2 || axis != ndim - 2))
-    return pk::fail("transposed storage needs axis == ndim - 2");
-  QuantParams p{};
-  p.x = x;
-  p.meta_gm = (layout & PK_LAYOUT_META_TRANSPOSED) != 0;
-  p.codes_tm = (layout & PK_LAYOUT_CODES_TRANSPOSED) != 0;
-  p.meta_d = ndim >= 2 ? shape[ndim - 1] : 1;
-  p.dtype = dtype;
-  p.len = shape[axis];
-  p.ax_stride = strides[axis];
-  p.rows = 1;
-  int n = 0;
-  for (int d = 0; d < ndim; ++d) {
-    if (shape[d] < 0) return pk::fail("negative dimension");
-    if (d == axis) continue;
-    p.pre_size[n] = shape[d];
-    p.pre_stride[n] = strides[d];
-    p.rows *= shape[d];
-    ++n;
-  }
-  p.npre = n;
-  if (p.len <= 0 || p.rows == 0) {
-    if (p.len <= 0) return pk::fail("quantized axis must be non-empty");
-    return PK_OK;
-  }
-  if (group_size <= 0 || group_size > p.len) return pk::fail("group_size must be in [1, len]");
-  if (!x || !out_packed || !out_scale || !out_mins) return pk::fail("null pointer");
-  p.bits = bits;
-  p.gs = group_size;
-  p.ngroups = pk::cdiv(p.len, group_size);
-  p.nbytes = pk::cdiv(p.len, 8 / bits);
-  // Threads walk adjacent rows when the quantized axis is not the contiguous one,
-  // so neighbouring lanes read neighbouring addresses.
-  p.rows_fastest = (p.ax_stride != 1) ? 1 : 0;
-  p.packed = out_packed;
-  p.scale = out_scale;
-  p.mins = out_mins;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  // the cache's layouts: fp16, contiguous, whole groups of 32 along the last or
-  // second-to-last axis
-  bool contiguous = true;
-  {
-    int64_t expect = 1;
-    for (int d = ndim - 1; d >= 0; --d) {
-      if (shape[d] != 1 && strides[d] != expect) contiguous = false;
-      expect *= shape[d];
+  return pk::guarded("pk_quantize_pack", [&]() -> int {
+    pk::clear_error();
+    if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+    if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16 && dtype != PK_DTYPE_F32)
+      return pk::fail("x must be float16, bfloat16 or float32");
+    if (ndim < 1 || ndim > kMaxDims) return pk::fail("x must have 1..8 dims");
+    if (axis < 0 || axis >= ndim) return pk::fail("axis out of range");
+    if (layout & ~(PK_LAYOUT_META_TRANSPOSED | PK_LAYOUT_CODES_TRANSPOSED))
+      return pk::fail("unknown layout flags");
+    if (layout && (ndim < 2 || axis != ndim - 2))
+      return pk::fail("transposed storage needs axis == ndim - 2");
+    QuantParams p{};
+    p.x = x;
+    p.meta_gm = (layout & PK_LAYOUT_META_TRANSPOSED) != 0;
+    p.codes_tm = (layout & PK_LAYOUT_CODES_TRANSPOSED) != 0;
+    p.meta_d = ndim >= 2 ? shape[ndim - 1] : 1;
+    p.dtype = dtype;
+    p.len = shape[axis];
+    p.ax_stride = strides[axis];
+    p.rows = 1;
+    int n = 0;
+    for (int d = 0; d < ndim; ++d) {
+      if (shape[d] < 0) return pk::fail("negative dimension");
+      if (d == axis) continue;
+      p.pre_size[n] = shape[d];
+      p.pre_stride[n] = strides[d];
+      p.rows *= shape[d];
+      ++n;
     }
-  }
-  const bool fast = dtype == PK_DTYPE_F16 && contiguous && group_size == 32 && p.len % 32 == 0 &&
-                    reinterpret_cast<uintptr_t>(x) % 16 == 0;
-  if (fast && axis == ndim - 1 && !layout) {
-    const int64_t lanes = p.rows * p.ngroups * 4;
-#define PK_INNER(B) hipLaunchKernelGGL(quantize_inner32_kernel<B>, dim3(grid_for(lanes)), dim3(kThreads), \
-                                       0, s, static_cast<const uint16_t*>(x), p.rows, p.len, p.ngroups, \
-                                       p.nbytes, out_packed, out_scale, out_mins)
-    if (bits == 2) PK_INNER(2); else if (bits == 4) PK_INNER(4); else PK_INNER(8);
-#undef PK_INNER
+    p.npre = n;
+    if (p.len <= 0 || p.rows == 0) {
+      if (p.len <= 0) return pk::fail("quantized axis must be non-empty");
+      return PK_OK;
+    }
+    if (group_size <= 0 || group_size > p.len) return pk::fail("group_size must be in [1, len]");
+    if (!x || !out_packed || !out_scale || !out_mins) return pk::fail("null pointer");
+    p.bits = bits;
+    p.gs = group_size;
+    p.ngroups = pk::cdiv(p.len, group_size);
+    p.nbytes = pk::cdiv(p.len, 8 / bits);
+    // Threads walk adjacent rows when the quantized axis is not the contiguous one,
+    // so neighbouring lanes read neighbouring addresses.
+    p.rows_fastest = (p.ax_stride != 1) ? 1 : 0;
+    p.packed = out_packed;
+    p.scale = out_scale;
+    p.mins = out_mins;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // the cache's layouts: fp16, contiguous, whole groups of 32 along the last or
+    // second-to-last axis
+    bool contiguous = true;
+    {
+      int64_t expect = 1;
+      for (int d = ndim - 1; d >= 0; --d) {
+        if (shape[d] != 1 && strides[d] != expect) contiguous = false;
+        expect *= shape[d];
+      }
+    }
+    const bool fast = dtype == PK_DTYPE_F16 && contiguous && group_size == 32 && p.len % 32 == 0 &&
+                      reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (fast && axis == ndim - 1 && !layout) {
+      const int64_t lanes = p.rows * p.ngroups * 4;
+  #define PK_INNER(B) hipLaunchKernelGGL(quantize_inner32_kernel<B>, dim3(grid_for(lanes)), dim3(kThreads), \
+                                         0, s, static_cast<const uint16_t*>(x), p.rows, p.len, p.ngroups, \
+                                         p.nbytes, out_packed, out_scale, out_mins)
+      if (bits == 2) PK_INNER(2); else if (bits == 4) PK_INNER(4); else PK_INNER(8);
+  #undef PK_INNER
+      return pk::check_launch("quantize_pack");
+    }
+    if (fast && axis == ndim - 2 && shape[ndim - 1] % 2 == 0) {
+      const int64_t D = shape[ndim - 1];
+      const int64_t outer = p.rows / D;
+      const int64_t threads = outer * p.ngroups * (D / 2) * 4;
+  #define PK_OUTER(B) hipLaunchKernelGGL(quantize_outer32_kernel<B>, dim3(grid_for(threads)), dim3(kThreads), \
+                                         0, s, static_cast<const uint16_t*>(x), outer, p.len, D, p.ngroups, \
+                                         p.nbytes, out_packed, out_scale, out_mins, p.meta_gm, p.codes_tm)
+      if (bits == 2) PK_OUTER(2); else if (bits == 4) PK_OUTER(4); else PK_OUTER(8);
+  #undef PK_OUTER
+      return pk::check_launch("quantize_pack");
+    }
+    if (group_size % (8 / bits) == 0) {
+      hipLaunchKernelGGL(quantize_groups_kernel, dim3(grid_for(p.rows * p.ngroups)),
+                         dim3(kThreads), 0, s, p);
+    } else {
+      hipLaunchKernelGGL(quantize_meta_kernel, dim3(grid_for(p.rows * p.ngroups)), dim3(kThreads),
+                         0, s, p);
+      int rc = pk::check_launch("quantize_pack(meta)");
+      if (rc) return rc;
+      hipLaunchKernelGGL(quantize_bytes_kernel, dim3(grid_for(p.rows * p.nbytes)), dim3(kThreads),
+                         0, s, p);
+    }
     return pk::check_launch("quantize_pack");
-  }
-  if (fast && axis == ndim - 2 && shape[ndim - 1] % 2 == 0) {
-    const int64_t D = shape[ndim - 1];
-    const int64_t outer = p.rows / D;
-    const int64_t threads = outer * p.ngroups * (D / 2) * 4;
-#define PK_OUTER(B) hipLaunchKernelGGL(quantize_outer32_kernel<B>, dim3(grid_for(threads)), dim3(kThreads), \
-                                       0, s, static_cast<const uint16_t*>(x), outer, p.len, D, p.ngroups, \
-                                       p.nbytes, out_packed, out_scale, out_mins, p.meta_gm, p.codes_tm)
-    if (bits == 2) PK_OUTER(2); else if (bits == 4) PK_OUTER(4); else PK_OUTER(8);
-#undef PK_OUTER
-    return pk::check_launch("quantize_pack");
-  }
-  if (group_size % (8 / bits) == 0) {
-    hipLaunchKernelGGL(quantize_groups_kernel, dim3(grid_for(p.rows * p.ngroups)),
-                       dim3(kThreads), 0, s, p);
-  } else {
-    hipLaunchKernelGGL(quantize_meta_kernel, dim3(grid_for(p.rows * p.ngroups)), dim3(kThreads),
-                       0, s, p);
-    int rc = pk::check_launch("quantize_pack(meta)");
-    if (rc) return rc;
-    hipLaunchKernelGGL(quantize_bytes_kernel, dim3(grid_for(p.rows * p.nbytes)), dim3(kThreads),
-                       0, s, p);
-  }
-  return pk::check_launch("quantize_pack");
+  });
 }
 
 extern "C" int pk_quantize_pack_kv(const uint16_t* k, const uint16_t* v, int batch,
@@ -564,64 +570,68 @@ extern "C" int pk_quantize_pack_kv(const uint16_t* k, const uint16_t* v, int bat
                                    uint8_t* k_packed, uint16_t* k_scale, uint16_t* k_mins,
                                    uint8_t* v_packed, uint16_t* v_scale, uint16_t* v_mins,
                                    void* stream) {
-  pk::clear_error();
-  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
-  if (!k || !v || !k_packed || !k_scale || !k_mins || !v_packed || !v_scale || !v_mins)
-    return pk::fail("null K / V / output pointer");
-  if (batch <= 0 || num_kv_heads <= 0 || seq_len <= 0 || head_dim <= 0)
-    return pk::fail("batch, num_kv_heads, seq_len and head_dim must be positive");
-  if (seq_len % 32 || head_dim % 32)
-    return pk::fail("the one-launch K/V pack needs seq_len and head_dim multiples of 32");
-  if (reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(v) % 16 ||
-      reinterpret_cast<uintptr_t>(k_packed) % 4 || reinterpret_cast<uintptr_t>(v_packed) % 4)
-    return pk::fail("K / V must be 16-byte aligned and the code buffers 4-byte aligned");
-  KVPackArgs a{k, v, (int64_t)batch * num_kv_heads, seq_len, head_dim, k_packed, k_scale,
-               k_mins, v_packed, v_scale, v_mins, 0};
-  const int64_t k_lanes = a.outer * (seq_len / 32) * (head_dim / 2) * 4;
-  const int64_t v_lanes = a.outer * seq_len * (head_dim / 32) * 4;
-  a.k_blocks = grid_for(k_lanes);
-  const int grid = a.k_blocks + grid_for(v_lanes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (bits == 2)
-    hipLaunchKernelGGL(quantize_kv32_kernel<2>, dim3(grid), dim3(kThreads), 0, s, a);
-  else if (bits == 4)
-    hipLaunchKernelGGL(quantize_kv32_kernel<4>, dim3(grid), dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(quantize_kv32_kernel<8>, dim3(grid), dim3(kThreads), 0, s, a);
-  return pk::check_launch("quantize_pack_kv");
+  return pk::guarded("pk_quantize_pack_kv", [&]() -> int {
+    pk::clear_error();
+    if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+    if (!k || !v || !k_packed || !k_scale || !k_mins || !v_packed || !v_scale || !v_mins)
+      return pk::fail("null K / V / output pointer");
+    if (batch <= 0 || num_kv_heads <= 0 || seq_len <= 0 || head_dim <= 0)
+      return pk::fail("batch, num_kv_heads, seq_len and head_dim must be positive");
+    if (seq_len % 32 || head_dim % 32)
+      return pk::fail("the one-launch K/V pack needs seq_len and head_dim multiples of 32");
+    if (reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(v) % 16 ||
+        reinterpret_cast<uintptr_t>(k_packed) % 4 || reinterpret_cast<uintptr_t>(v_packed) % 4)
+      return pk::fail("K / V must be 16-byte aligned and the code buffers 4-byte aligned");
+    KVPackArgs a{k, v, (int64_t)batch * num_kv_heads, seq_len, head_dim, k_packed, k_scale,
+                 k_mins, v_packed, v_scale, v_mins, 0};
+    const int64_t k_lanes = a.outer * (seq_len / 32) * (head_dim / 2) * 4;
+    const int64_t v_lanes = a.outer * seq_len * (head_dim / 32) * 4;
+    a.k_blocks = grid_for(k_lanes);
+    const int grid = a.k_blocks + grid_for(v_lanes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (bits == 2)
+      hipLaunchKernelGGL(quantize_kv32_kernel<2>, dim3(grid), dim3(kThreads), 0, s, a);
+    else if (bits == 4)
+      hipLaunchKernelGGL(quantize_kv32_kernel<4>, dim3(grid), dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL(quantize_kv32_kernel<8>, dim3(grid), dim3(kThreads), 0, s, a);
+    return pk::check_launch("quantize_pack_kv");
+  });
 }
 
 extern "C" int pk_unpack_dequantize(const uint8_t* packed, const uint16_t* scale,
                                     const uint16_t* mins, int ndim, const int64_t* orig_shape,
                                     int axis, int bits, int group_size, int64_t n_groups,
                                     uint16_t* out, void* stream) {
-  pk::clear_error();
-  if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
-  if (ndim < 1 || ndim > kMaxDims) return pk::fail("orig_shape must have 1..8 dims");
-  if (axis < 0 || axis >= ndim) return pk::fail("axis out of range");
-  DequantParams p{};
-  p.ndim = ndim;
-  p.axis = axis;
-  p.total = 1;
-  for (int d = 0; d < ndim; ++d) {
-    if (orig_shape[d] < 0) return pk::fail("negative dimension");
-    p.shape[d] = orig_shape[d];
-    p.total *= orig_shape[d];
-  }
-  p.len = orig_shape[axis];
-  if (p.total == 0) return PK_OK;
-  if (group_size <= 0) return pk::fail("group_size must be positive");
-  if (n_groups * group_size < p.len) return pk::fail("scale/mins hold fewer groups than the axis needs");
-  if (!packed || !scale || !mins || !out) return pk::fail("null pointer");
-  p.packed = packed;
-  p.scale = scale;
-  p.mins = mins;
-  p.bits = bits;
-  p.gs = group_size;
-  p.ngroups = n_groups;
-  p.nbytes = pk::cdiv(p.len, 8 / bits);
-  p.out = out;
-  hipLaunchKernelGGL(unpack_dequantize_kernel, dim3(grid_for(p.total)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), p);
-  return pk::check_launch("unpack_dequantize");
+  return pk::guarded("pk_unpack_dequantize", [&]() -> int {
+    pk::clear_error();
+    if (!pk::valid_bits(bits)) return pk::fail("bits must be one of (2, 4, 8)");
+    if (ndim < 1 || ndim > kMaxDims) return pk::fail("orig_shape must have 1..8 dims");
+    if (axis < 0 || axis >= ndim) return pk::fail("axis out of range");
+    DequantParams p{};
+    p.ndim = ndim;
+    p.axis = axis;
+    p.total = 1;
+    for (int d = 0; d < ndim; ++d) {
+      if (orig_shape[d] < 0) return pk::fail("negative dimension");
+      p.shape[d] = orig_shape[d];
+      p.total *= orig_shape[d];
+    }
+    p.len = orig_shape[axis];
+    if (p.total == 0) return PK_OK;
+    if (group_size <= 0) return pk::fail("group_size must be positive");
+    if (n_groups * group_size < p.len) return pk::fail("scale/mins hold fewer groups than the axis needs");
+    if (!packed || !scale || !mins || !out) return pk::fail("null pointer");
+    p.packed = packed;
+    p.scale = scale;
+    p.mins = mins;
+    p.bits = bits;
+    p.gs = group_size;
+    p.ngroups = n_groups;
+    p.nbytes = pk::cdiv(p.len, 8 / bits);
+    p.out = out;
+    hipLaunchKernelGGL(unpack_dequantize_kernel, dim3(grid_for(p.total)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), p);
+    return pk::check_launch("unpack_dequantize");
+  });
 }

@@ -285,65 +285,69 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
 extern "C" int pk_prompt_votes(const void* attention, int dtype, int64_t batch, int64_t num_q_heads,
                                int64_t q_len, int64_t kv_len, const int64_t* strides,
                                int num_kv_heads, int obs_window, float* votes, void* stream) {
-  pk::clear_error();
-  if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16 && dtype != PK_DTYPE_F32)
-    return pk::fail("attention must be float16, bfloat16 or float32");
-  if (batch <= 0 || num_q_heads <= 0 || q_len <= 0 || kv_len <= 0 || num_kv_heads <= 0)
-    return pk::fail("attention shape and kv heads must be positive");
-  if (num_q_heads % num_kv_heads) return pk::fail("query heads must be a multiple of kv heads");
-  if (obs_window <= 0) return pk::fail("obs_window must be positive");
-  if (!attention || !votes || !strides) return pk::fail("null pointer");
-  if (num_q_heads / num_kv_heads > kMaxGroup) return pk::fail("more than 32 query heads per kv head");
-  const int w = (int)std::min<int64_t>(obs_window, q_len);
-  AttnView a{attention, dtype, strides[0], strides[1], strides[2], strides[3]};
-  const int G = (int)(num_q_heads / num_kv_heads);
-  // 4 keys per lane in one 8-byte load for 16-bit attention with contiguous,
-  // 8-byte aligned key rows of a multiple of 4 keys; else one key per lane
-  const bool vec = dtype != PK_DTYPE_F32 && strides[3] == 1 && kv_len % 4 == 0 &&
-                   strides[0] % 4 == 0 && strides[1] % 4 == 0 && strides[2] % 4 == 0 &&
-                   reinterpret_cast<uintptr_t>(attention) % 8 == 0;
-  // 2 keys per lane (4-byte loads) when 4 per lane would leave CUs without a workgroup
-  int kpl = vec ? 4 : 1;
-  if (vec && batch * num_kv_heads * pk::cdiv(kv_len, 64 * 4) < pk::device_cu_count()) kpl = 2;
-  const int64_t blocks = batch * num_kv_heads * pk::cdiv(kv_len, 64 * kpl);
-  if (blocks > 0x7fffffff) return pk::fail("attention too large");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (kpl == 4)
-    hipLaunchKernelGGL(votes_kernel<4>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
-                       num_kv_heads, G, q_len, kv_len, w, votes);
-  else if (kpl == 2)
-    hipLaunchKernelGGL(votes_kernel<2>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
-                       num_kv_heads, G, q_len, kv_len, w, votes);
-  else
-    hipLaunchKernelGGL(votes_kernel<1>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
-                       num_kv_heads, G, q_len, kv_len, w, votes);
-  return pk::check_launch("prompt_votes");
+  return pk::guarded("pk_prompt_votes", [&]() -> int {
+    pk::clear_error();
+    if (dtype != PK_DTYPE_F16 && dtype != PK_DTYPE_BF16 && dtype != PK_DTYPE_F32)
+      return pk::fail("attention must be float16, bfloat16 or float32");
+    if (batch <= 0 || num_q_heads <= 0 || q_len <= 0 || kv_len <= 0 || num_kv_heads <= 0)
+      return pk::fail("attention shape and kv heads must be positive");
+    if (num_q_heads % num_kv_heads) return pk::fail("query heads must be a multiple of kv heads");
+    if (obs_window <= 0) return pk::fail("obs_window must be positive");
+    if (!attention || !votes || !strides) return pk::fail("null pointer");
+    if (num_q_heads / num_kv_heads > kMaxGroup) return pk::fail("more than 32 query heads per kv head");
+    const int w = (int)std::min<int64_t>(obs_window, q_len);
+    AttnView a{attention, dtype, strides[0], strides[1], strides[2], strides[3]};
+    const int G = (int)(num_q_heads / num_kv_heads);
+    // 4 keys per lane in one 8-byte load for 16-bit attention with contiguous,
+    // 8-byte aligned key rows of a multiple of 4 keys; else one key per lane
+    const bool vec = dtype != PK_DTYPE_F32 && strides[3] == 1 && kv_len % 4 == 0 &&
+                     strides[0] % 4 == 0 && strides[1] % 4 == 0 && strides[2] % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(attention) % 8 == 0;
+    // 2 keys per lane (4-byte loads) when 4 per lane would leave CUs without a workgroup
+    int kpl = vec ? 4 : 1;
+    if (vec && batch * num_kv_heads * pk::cdiv(kv_len, 64 * 4) < pk::device_cu_count()) kpl = 2;
+    const int64_t blocks = batch * num_kv_heads * pk::cdiv(kv_len, 64 * kpl);
+    if (blocks > 0x7fffffff) return pk::fail("attention too large");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (kpl == 4)
+      hipLaunchKernelGGL(votes_kernel<4>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+                         num_kv_heads, G, q_len, kv_len, w, votes);
+    else if (kpl == 2)
+      hipLaunchKernelGGL(votes_kernel<2>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+                         num_kv_heads, G, q_len, kv_len, w, votes);
+    else
+      hipLaunchKernelGGL(votes_kernel<1>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+                         num_kv_heads, G, q_len, kv_len, w, votes);
+    return pk::check_launch("prompt_votes");
+  });
 }
 
 extern "C" int pk_select_prompt(const float* votes, int64_t rows, int64_t kv_len, int64_t sink,
                                 int64_t recent_start, int64_t select_k, int pool_kernel,
                                 int pool_mode, int64_t* keep, void* stream) {
-  pk::clear_error();
-  if (rows <= 0 || kv_len <= 0) return pk::fail("rows and kv_len must be positive");
-  if (sink < 0 || recent_start < sink || recent_start > kv_len)
-    return pk::fail("need 0 <= sink <= recent_start <= kv_len");
-  if (select_k < 0 || select_k > recent_start - sink)
-    return pk::fail("select_k must lie in [0, recent_start - sink]");
-  if (pool_mode != 0 && pool_mode != 1) return pk::fail("pool_mode must be 0 (max) or 1 (avg)");
-  if (!votes || !keep) return pk::fail("null pointer");
-  const int64_t budget = sink + select_k + (kv_len - recent_start);
-  const int64_t n = recent_start - sink;
-  const int staged = n <= kMaxStagedKeys ? 1 : 0;
-  const size_t lds = staged ? (size_t)n * 8 : 0;
-  static bool lds_opt_in = [] {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel),
-                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)(kMaxStagedKeys * 8)) == hipSuccess;
-  }();
-  if (staged && lds > 64 * 1024 && !lds_opt_in)
-    return pk::fail("cannot reserve the selection kernel's LDS"), PK_ERR_RUNTIME;
-  hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(kPickThreads), lds,
-                     static_cast<hipStream_t>(stream), votes, kv_len, sink, recent_start,
-                     select_k, pool_kernel, pool_mode, keep, budget, staged);
-  return pk::check_launch("select_prompt");
+  return pk::guarded("pk_select_prompt", [&]() -> int {
+    pk::clear_error();
+    if (rows <= 0 || kv_len <= 0) return pk::fail("rows and kv_len must be positive");
+    if (sink < 0 || recent_start < sink || recent_start > kv_len)
+      return pk::fail("need 0 <= sink <= recent_start <= kv_len");
+    if (select_k < 0 || select_k > recent_start - sink)
+      return pk::fail("select_k must lie in [0, recent_start - sink]");
+    if (pool_mode != 0 && pool_mode != 1) return pk::fail("pool_mode must be 0 (max) or 1 (avg)");
+    if (!votes || !keep) return pk::fail("null pointer");
+    const int64_t budget = sink + select_k + (kv_len - recent_start);
+    const int64_t n = recent_start - sink;
+    const int staged = n <= kMaxStagedKeys ? 1 : 0;
+    const size_t lds = staged ? (size_t)n * 8 : 0;
+    static bool lds_opt_in = [] {
+      return hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)(kMaxStagedKeys * 8)) == hipSuccess;
+    }();
+    if (staged && lds > 64 * 1024 && !lds_opt_in)
+      return pk::fail("cannot reserve the selection kernel's LDS"), PK_ERR_RUNTIME;
+    hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(kPickThreads), lds,
+                       static_cast<hipStream_t>(stream), votes, kv_len, sink, recent_start,
+                       select_k, pool_kernel, pool_mode, keep, budget, staged);
+    return pk::check_launch("select_prompt");
+  });
 }

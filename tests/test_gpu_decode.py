@@ -121,15 +121,47 @@ def test_c2_against_fp16_materialized_reference(gpu):
     _close(out, want.astype(np.float64))
 
 
-@pytest.mark.parametrize("prompt", [32768])
-def test_c3_long_context_matches_oracle(gpu, prompt):
+@pytest.mark.parametrize("name", ["C3-4K", "C3-8K", "C3-16K", "C3-32K"])
+def test_c3_long_context_matches_oracle(gpu, name):
+    """The context sweep exactly as benchmarked (prompt 4K-32K @2-bit, cold 512 @4-bit, hot 128)."""
     from phasekv_amd.kernels.attention_triton import fused_phasekv_decode
     from phasekv_amd import workloads
-    cfg = replace(workloads.CONFIGS["C3-32K"], prompt=prompt)
+    cfg = workloads.CONFIGS[name]
+    print(f"case {name}", flush=True)
     wl = workloads.make_workload(cfg, gpu)
     out = fused_phasekv_decode(wl.q[0], wl.tiers, cfg.hq)
     want = ao.layer_tiers_attention(wl.q[0].cpu().numpy(), _oracle_tiers(wl.tiers), cfg.hq)
     _close(out, want)
+
+
+def _row_tiers(t, b, prompt_len):
+    """Oracle tiers of batch row b, its prompt cut to the row's valid length."""
+    def cut(pt, axis_len):
+        if pt.axis == 2:    # K: codes / groups along tokens in the last dim
+            vpb = 8 // pt.bits
+            return po.PackedArrays(pt.packed[b:b + 1, :, :, :-(-axis_len // vpb)],
+                                   pt.scale[b:b + 1, :, :, :-(-axis_len // pt.group_size)],
+                                   pt.mins[b:b + 1, :, :, :-(-axis_len // pt.group_size)],
+                                   pt.bits, 2, pt.group_size,
+                                   (1,) + pt.orig_shape[1:2] + (axis_len,) + pt.orig_shape[3:],
+                                   axis_len)
+        return po.PackedArrays(pt.packed[b:b + 1, :, :axis_len], pt.scale[b:b + 1, :, :axis_len],
+                               pt.mins[b:b + 1, :, :axis_len], pt.bits, 3, pt.group_size,
+                               (1,) + pt.orig_shape[1:2] + (axis_len,) + pt.orig_shape[3:],
+                               pt.axis_len)
+    seg = lambda s, n: ao.SegmentArrays(cut(s.key, n), cut(s.value, n))
+    return ao.LayerTiersArrays(seg(t.prompt, prompt_len),
+                               [seg(s, s.key.axis_len) for s in t.prompt_extensions],
+                               [seg(s, s.key.axis_len) for s in t.cold],
+                               t.hot_k[b:b + 1], t.hot_v[b:b + 1])
+
+
+def _check_batched(wl, out):
+    t = _oracle_tiers(wl.tiers)
+    q = wl.q.cpu().numpy()
+    for b, L in enumerate(wl.prompt_lens_list):
+        print(f"  row {b} prompt {L}", flush=True)
+        _close(out[b], ao.layer_tiers_attention(q[b], _row_tiers(t, b, L), wl.cfg.hq))
 
 
 def test_batched_ragged_matches_per_row_oracle(gpu):
@@ -138,30 +170,7 @@ def test_batched_ragged_matches_per_row_oracle(gpu):
     from phasekv_amd import workloads
     cfg = replace(workloads.CONFIGS["C4"], batch=4, prompt=1024, ragged_min=300, cold=96, hot=64)
     wl = workloads.make_workload(cfg, gpu)
-    out = fused_phasekv_decode_batched(wl.q, wl.tiers, cfg.hq, wl.prompt_lens)
-    t = _oracle_tiers(wl.tiers)
-    for b, L in enumerate(wl.prompt_lens_list):
-        def cut(pt, axis_len):
-            # row b, prompt truncated to its valid length (K: codes along tokens)
-            if pt.axis == 2:
-                vpb = 8 // pt.bits
-                return po.PackedArrays(pt.packed[b:b + 1, :, :, :-(-axis_len // vpb)],
-                                       pt.scale[b:b + 1, :, :, :-(-axis_len // pt.group_size)],
-                                       pt.mins[b:b + 1, :, :, :-(-axis_len // pt.group_size)],
-                                       pt.bits, 2, pt.group_size,
-                                       (1,) + pt.orig_shape[1:2] + (axis_len,) + pt.orig_shape[3:],
-                                       axis_len)
-            return po.PackedArrays(pt.packed[b:b + 1, :, :axis_len], pt.scale[b:b + 1, :, :axis_len],
-                                   pt.mins[b:b + 1, :, :axis_len], pt.bits, 3, pt.group_size,
-                                   (1,) + pt.orig_shape[1:2] + (axis_len,) + pt.orig_shape[3:],
-                                   pt.axis_len)
-        row = ao.LayerTiersArrays(
-            ao.SegmentArrays(cut(t.prompt.key, L), cut(t.prompt.value, L)), [],
-            [ao.SegmentArrays(cut(s.key, s.key.axis_len), cut(s.value, s.key.axis_len))
-             for s in t.cold],
-            t.hot_k[b:b + 1], t.hot_v[b:b + 1])
-        want = ao.layer_tiers_attention(wl.q[b].cpu().numpy(), row, cfg.hq)
-        _close(out[b], want)
+    _check_batched(wl, fused_phasekv_decode_batched(wl.q, wl.tiers, cfg.hq, wl.prompt_lens))
 
 
 def test_c5_shape_batched_student_t(gpu):
@@ -169,16 +178,23 @@ def test_c5_shape_batched_student_t(gpu):
     from phasekv_amd import workloads
     cfg = replace(workloads.CONFIGS["C5"], batch=2, prompt=2048, cold=256, hot=64)
     wl = workloads.make_workload(cfg, gpu)
-    out = fused_phasekv_decode_batched(wl.q, wl.tiers, cfg.hq)
-    t = _oracle_tiers(wl.tiers)
-    for b in range(cfg.batch):
-        sl = lambda pt: po.PackedArrays(pt.packed[b:b + 1], pt.scale[b:b + 1], pt.mins[b:b + 1],
-                                        pt.bits, pt.axis, pt.group_size,
-                                        (1,) + tuple(pt.orig_shape[1:]), pt.axis_len)
-        row = ao.LayerTiersArrays(ao.SegmentArrays(sl(t.prompt.key), sl(t.prompt.value)), [],
-                                  [ao.SegmentArrays(sl(s.key), sl(s.value)) for s in t.cold],
-                                  t.hot_k[b:b + 1], t.hot_v[b:b + 1])
-        _close(out[b], ao.layer_tiers_attention(wl.q[b].cpu().numpy(), row, cfg.hq))
+    _check_batched(wl, fused_phasekv_decode_batched(wl.q, wl.tiers, cfg.hq))
+
+
+@pytest.mark.parametrize("name", ["C4", "C5"])
+def test_batched_configs_full_size_match_oracle(gpu, name):
+    """C4 (batch 16, ragged prompts of 4096-8192 tokens @4-bit, cold 1024 @2-bit, hot 64)
+    and C5 (batch 8, Llama-3-8B heads, prompt 16384 @2-bit, cold 2048 @8-bit, hot 256)
+    exactly as benchmarked: the oversubscribed chunk-major launch and the long pipelined
+    wave loops run only at these sizes.  Every batch row against the oracle."""
+    from phasekv_amd.kernels.attention_triton import fused_phasekv_decode_batched
+    from phasekv_amd import workloads
+    cfg = workloads.CONFIGS[name]
+    print(f"case {name} full size {cfg}", flush=True)
+    wl = workloads.make_workload(cfg, gpu)
+    out = fused_phasekv_decode_batched(wl.q, wl.tiers, cfg.hq, wl.prompt_lens)
+    torch.cuda.synchronize()
+    _check_batched(wl, out)
 
 
 def test_legacy_per_token_entry_points(gpu):

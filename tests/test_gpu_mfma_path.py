@@ -141,3 +141,66 @@ def test_mfma_long_wave_runs(gpu, hd, length):
     want = ao.segments_attention(q[0].numpy(), [(deq_k, deq_v)], hq)
     np.testing.assert_allclose(fast, want, atol=2e-3, rtol=1e-2)
     np.testing.assert_allclose(fast, slow, atol=1e-3, rtol=1e-2)
+
+
+def _ramp_tiers(gpu, g, hq, hkv, hd, length, kb, vb, v_range, big_q):
+    """Scores that climb along the segment (so the running maximum keeps lagging the
+    group maxima by up to the lazy bound) over V rows whose channel groups span
+    ``v_range``.  With ``big_q``, q channel 5 is large and K channel 5 spans a range whose
+    scale times that q is beyond fp16 in one group (tokens 320..351, which then holds the
+    largest scores) and below it everywhere else."""
+    from phasekv_amd import decode as dec
+    from phasekv_amd.kernels.packing import quantize_pack
+    q = torch.randn(1, hq, hd, generator=g)
+    k = torch.randn(1, hkv, length, hd, generator=g)
+    # k . q grows along the tokens: a component along each head group's mean q direction
+    dirs = q[0].view(hkv, hq // hkv, hd).mean(1)
+    dirs = dirs / dirs.norm(dim=-1, keepdim=True)
+    ramp = torch.linspace(0.0, 60.0, length)
+    k += ramp[None, None, :, None] * dirs[None, :, None, :]
+    if big_q:
+        # (q, range of the special group, range elsewhere) per K width: q * scale is about
+        # 3e5 (9e4 at 8 bits) in the special group and at most 5e4 elsewhere.  In the
+        # special group token 330 alone takes the top code of channel 5, so it holds
+        # the largest score by far (a well-conditioned one-hot softmax)
+        qv, r_s, r_o = {2: (300.0, 3000.0, 500.0), 4: (300.0, 15000.0, 2500.0),
+                        8: (2000.0, 12000.0, 1500.0)}[kb]
+        q[..., 5] = qv
+        u = torch.rand(1, hkv, length, generator=g) - 0.5
+        k[..., 5] = u * r_o
+        k[..., 320:352, 5] = (u[..., 320:352] - 0.5) * (r_s / 2)
+        k[..., 321, 5] = -r_s / 2
+        k[..., 330, 5] = r_s / 2
+    v = torch.randn(1, hkv, length, hd, generator=g)
+    v[..., ::3, :32] *= v_range / 6.0          # wide channel groups on every third token
+    v = v.clamp(-65000.0, 65000.0)
+    q, k, v = (x.to(torch.float16) for x in (q, k, v))
+    pk = quantize_pack(k.to(gpu), kb, -2, 32)
+    pv = quantize_pack(v.to(gpu), vb, -1, 32)
+    # one chunk per head group: every wave runs many groups, so the lagging maximum
+    # lets p reach the lazy bound
+    return q, pk, pv, dec.packed_segment(pk, pv, batched=True, splits=1)
+
+
+@pytest.mark.parametrize("kb,vb", [(2, 2), (2, 4), (4, 4), (2, 8), (8, 8)])
+@pytest.mark.parametrize("case", ["wide_v", "big_q_times_k_scale"])
+def test_wide_ranges_stay_finite(gpu, kb, vb, case):
+    """Operands the MFMA path rounds to fp16 (q times the K scale, p times the V scale)
+    must not overflow: V groups whose scale is far above 2^8 with the lagging softmax
+    maximum, and a q channel times a K scale beyond 65504.  Against the oracle, which
+    computes in float64, at the north-star tolerance applied to the data rescaled to unit
+    range (the absolute bound scales with the largest |V|)."""
+    print(f"case {case} bits={kb},{vb}", flush=True)
+    g = torch.Generator().manual_seed(kb * 7 + vb)
+    hq, hkv, hd, length = 8, 2, 128, 1400
+    v_range = {2: 6000.0, 4: 40000.0, 8: 120000.0}[vb] if case == "wide_v" else 4.0
+    q, pk, pv, seg = _ramp_tiers(gpu, g, hq, hkv, hd, length, kb, vb, v_range,
+                                 case != "wide_v")
+    deq_k = po.dequantize_float(_np_pt(pk))[0]
+    deq_v = po.dequantize_float(_np_pt(pv))[0]
+    want = ao.segments_attention(q[0].numpy(), [(deq_k, deq_v)], hq)
+    assert np.isfinite(want).all()
+    fast = _run(q.to(gpu), [seg], hq, False)[0].float().cpu().numpy()
+    assert np.isfinite(fast).all(), "the MFMA path overflowed"
+    scale = max(1.0, float(np.abs(deq_v).max()))
+    np.testing.assert_allclose(fast, want, atol=2e-3 * scale, rtol=1e-2)
