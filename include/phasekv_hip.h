@@ -190,6 +190,18 @@ int pk_decode_combine(const pk_decode_problem* p, const void* workspace, uint16_
 int pk_fused_decode(const pk_decode_problem* p, void* workspace, size_t workspace_bytes,
                     uint16_t* out, void* stream);
 
+/* pk_fused_decode without a caller workspace and without any allocation: the
+ * split-K partials go to a file-scope device array of PK_NOALLOC_SCRATCH_BYTES
+ * (16 MiB) that each GPU the library runs on holds until the process ends.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Problems whose workspace (pk_decode_workspace_size)
+ * exceeds the array fail with PK_ERR_INVALID before any launch.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads) race; calls ordered on one stream do not. */
+#define PK_NOALLOC_SCRATCH_BYTES (16u << 20)
+int pk_fused_decode_noalloc(const pk_decode_problem* p, uint16_t* out, void* stream);
+
 /* Merge n partials per row: m, l [rows, n] and acc [rows, n, hd] fp32 contiguous.
  * Writes normalized fp16 out [rows, hd] (_merge_partials, attention_triton.py:300-307)
  * or, when out is NULL, unnormalized (m, l, acc) (_reduce_splits,

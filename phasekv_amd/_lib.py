@@ -27,6 +27,7 @@ PK_SEG_TOKEN = 1
 PK_SEG_FP16 = 2
 
 PK_MAX_SEGMENTS_PER_LAUNCH = 8
+PK_NOALLOC_SCRATCH_BYTES = 16 << 20
 PK_FLAG_GENERIC_KERNEL = 1
 
 PK_META_CHANNEL_MAJOR = 0
@@ -100,6 +101,7 @@ _SIGNATURES = {
                                          _c_vp, _c_vp, _c_vp]),
     "pk_fused_decode": (ctypes.c_int, [ctypes.POINTER(PkDecodeProblem), _c_vp, ctypes.c_size_t,
                                        _c_vp, _c_vp]),
+    "pk_fused_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(PkDecodeProblem), _c_vp, _c_vp]),
     "pk_merge_partials": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32, _c_vp,
                                          _c_vp, _c_vp, _c_vp, _c_vp]),
     "pk_append_hot": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,

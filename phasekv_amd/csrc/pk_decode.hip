@@ -21,6 +21,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 namespace pk {
@@ -720,6 +721,67 @@ extern "C" int pk_fused_decode(const pk_decode_problem* p, void* workspace, size
                           reinterpret_cast<const float*>(ws + pl.off_acc),
                           (int64_t)p->batch * p->num_q_heads, pl.C, p->head_dim, out, nullptr,
                           nullptr, nullptr, s, "fused_decode");
+  });
+}
+
+// ---------------------------------------------------------------------------
+// pk_fused_decode_noalloc: the split-K workspace in a file-scope device array
+// (one per GPU, held until the process ends) instead of a caller buffer.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[PK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch[kMaxDevices] = {};   // the array's device address, per device
+
+// The scratch array's address on the current device (looked up once per device).
+int scratch_address(char** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error(std::string("hipGetDevice: ") + hipGetErrorString(e));
+    return PK_ERR_RUNTIME;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail("device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      return PK_ERR_RUNTIME;
+    }
+    g_scratch[dev] = static_cast<char*>(p);
+  }
+  *ptr = g_scratch[dev];
+  return PK_OK;
+}
+}  // namespace
+
+extern "C" int pk_fused_decode_noalloc(const pk_decode_problem* p, uint16_t* out, void* stream) {
+  return pk::guarded("pk_fused_decode_noalloc", [&]() -> int {
+    clear_error();
+    int rc = validate_problem(p);
+    if (rc) return rc;
+    if (!out) return fail("null output");
+    Plan pl = make_plan(p);
+    if (pl.bytes > (size_t)PK_NOALLOC_SCRATCH_BYTES)
+      return fail("the problem needs " + std::to_string(pl.bytes) +
+                  " bytes of split-K workspace; pk_fused_decode_noalloc holds " +
+                  std::to_string((size_t)PK_NOALLOC_SCRATCH_BYTES) +
+                  " (use pk_fused_decode with a caller workspace)");
+    char* ws = nullptr;
+    rc = scratch_address(&ws);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = launch_partials(p, pl, ws, s);
+    if (rc) return rc;
+    return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
+                          reinterpret_cast<const float*>(ws + pl.off_l),
+                          reinterpret_cast<const float*>(ws + pl.off_acc),
+                          (int64_t)p->batch * p->num_q_heads, pl.C, p->head_dim, out, nullptr,
+                          nullptr, nullptr, s, "fused_decode_noalloc");
   });
 }
 
