@@ -68,8 +68,8 @@ def _time_graph(fns, steps: int, warmup: int, stream) -> float:
     flushed (a write of twice the MALL), so the timed replay reads its copies from HBM even
     when it touches fewer copies than the caches hold."""
     with torch.cuda.stream(stream):
-        for f in fns[:2]:
-            f()                           # warm workspaces outside the capture
+        for f in fns:
+            f()       # warm workspaces and build every copy's problem outside the capture
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
@@ -152,6 +152,46 @@ def _bench_config(cfg, device, steps, warmup, stream, with_dense=True):
         del sets, probs, dfns, dense
     torch.cuda.empty_cache()
     return res, wl
+
+
+def _bench_long_generation(device, steps, warmup, stream, generated=1056):
+    """C2's cache after ``generated`` decode tokens with lazy cooling (lazy_g 16, keep all,
+    4-bit cold): 64 cold segments of 16 tokens beside the prompt, C2's cold tier and a
+    40-token window.  The decode attends the cold segments from the device segment table
+    (one partials launch), timed beside the same segments as one list of launches of up to
+    8 segments each."""
+    from phasekv_amd import decode as dec
+    from phasekv_amd import workloads
+    from phasekv_amd.kernels.attention_triton import _reused_problem, fused_phasekv_decode
+    base = workloads.CONFIGS["C2"]
+    wl = workloads.make_long_generation(base, generated, device)
+    cfg = wl.cfg
+    nbytes = workloads.tiers_algorithmic_bytes(wl.tiers, cfg.hq)
+    copies = _copies_for(nbytes, 96)
+    tiers = [wl.tiers] + [workloads.clone_tiers(wl.tiers) for _ in range(copies - 1)]
+    q = wl.q[0]
+    sec = _time_graph([lambda t=t: fused_phasekv_decode(q, t, cfg.hq) for t in tiers], steps,
+                      warmup, stream)
+    probs = [_reused_problem(q, t, cfg.hq) for t in tiers]
+    listed = [dec.Problem(q, [pr.segments[0], *pr.segments[1:-1], *pr.table.segments,
+                              pr.segments[-1]], cfg.hq) for pr in probs]
+    lsec = _time_graph([lambda pr=pr: dec.fused_decode(pr) for pr in listed], steps, warmup,
+                       stream)
+    ksec = _time_graph([lambda pr=pr: dec.launch_partials(pr) for pr in probs], steps, warmup,
+                       stream)
+    n_list = len(listed[0].segments)
+    res = {"config": cfg.name, "generated_tokens": generated,
+           "cold_segments": len(wl.tiers.cold), "table_entries": probs[0].table.count,
+           "tokens": cfg.prompt + cfg.cold + cfg.hot, "bytes": nbytes, "copies": copies,
+           "timed_distinct_bytes": min(steps, copies) * nbytes,
+           "us_per_step": sec * 1e6, "gbs": nbytes / sec / 1e9, "partials_launches": 1,
+           "partials_us": ksec * 1e6,
+           "listed_us_per_step": lsec * 1e6,
+           "listed_partials_launches": -(-n_list // 8),
+           "speedup_vs_listed": lsec / sec}
+    del tiers, probs, listed
+    torch.cuda.empty_cache()
+    return res
 
 
 def _bench_prefill_pack(device, steps, warmup, stream):
@@ -454,6 +494,8 @@ def main() -> int:
                     help="time per output token of the Qwen2 adapter against the dense cache")
     ap.add_argument("--prefill", action="store_true",
                     help="time only the prefill side (C4 pack, prompt selection) and print its line")
+    ap.add_argument("--long-generation", action="store_true",
+                    help="time only the C2 cache after 1056 generated tokens (64 cold segments)")
     ap.add_argument("--lifecycle", action="store_true",
                     help="time only the hot window lifecycle (append, cooling) and print its line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -492,6 +534,14 @@ def main() -> int:
                           "n_gpus": 1, "config": {"workload": "C4 prefill"}, "rows": rows}),
               flush=True)
         return 0
+    if args.long_generation:
+        r = _bench_long_generation(device, min(args.steps, 256), min(args.warmup, 256), stream)
+        r = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        print(json.dumps({"metric": "decode-attn µs/step, C2 cache after 1056 generated tokens",
+                          "value": r["us_per_step"], "unit": "µs", "higher_is_better": False,
+                          "n_gpus": 1, "config": {"workload": r["config"]}, "rows": [r]}),
+              flush=True)
+        return 0
     if args.lifecycle:
         rows = []
         for name, ratio in (("C2", 1.0), ("C2", 0.5), ("C5", 0.5)):
@@ -521,6 +571,9 @@ def main() -> int:
                 r["cpu_baseline"] = _cpu_baseline("C1", min(args.cpu_seconds, 5.0))
             _log(f"bench: {name} {r}")
             sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+        r = _bench_long_generation(device, min(args.steps, 256), min(args.warmup, 256), stream)
+        _log(f"bench: long generation {r}")
+        sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
         r = _bench_prefill_pack(device, min(args.steps, 128), min(args.warmup, 128), stream)
         _log(f"bench: C4-prefill-pack {r}")
         sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})

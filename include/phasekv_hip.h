@@ -155,9 +155,39 @@ typedef struct pk_decode_problem {
   const pk_segment* segments;  /* host array */
   int32_t num_segments;
   int32_t flags;               /* PK_FLAG_* */
+  /* Segments kept in device memory (pk_segment_table_write): entries [0, table_count) of
+   * `table` are attended besides `segments`, all in the same partials launch.  The
+   * entries must describe segments of this problem's batch, kv heads and head_dim.
+   * table_bits: the widest K or V code among them (2 or 4); 0 when table_count is 0. */
+  const void* table;
+  int32_t table_count;
+  int32_t table_bits;
 } pk_decode_problem;
 
 #define PK_FLAG_GENERIC_KERNEL 1   /* use the general-shape kernel even where the MFMA one applies */
+
+/* ---- device-resident segment table ------------------------------------------
+ * The cache's packed segments as descriptors in device memory, so that a decode
+ * step over any number of them is one partials launch with a fixed-size argument
+ * block.  The reference keeps a Python list of cold segments, one appended per
+ * cooling event (src/phasekv/phasekv_cache.py:322-340), and launches once per
+ * segment (src/phasekv/kernels/attention_triton.py:662-665).  A table is caller
+ * memory of pk_segment_table_entry_bytes() bytes per entry; entries are written
+ * on the stream (a small kernel: no host memory is read by the GPU, so the write
+ * can be captured in a graph) and read by decode launches ordered after it. */
+
+/* Bytes of one table entry. */
+size_t pk_segment_table_entry_bytes(void);
+
+/* Write entries [first, first + count) of `table` from segments[0 .. count).  Each
+ * must be a KIVI segment in the storage quantize_pack writes (token-major K codes,
+ * group-major K scale / min, 16-byte aligned code rows, V scale / min rows aligned to
+ * head_dim / 32 halves), K and V widths of 2 or 4 bits, V groups of 32 and K groups
+ * of 32 or a single group; otherwise PK_ERR_INVALID and nothing is written.
+ * head_dim: 64 or 128.  A decode attends each entry with one wave per segment, so
+ * the table suits many short segments (the cold segments of lazy cooling). */
+int pk_segment_table_write(void* table, int32_t first, int32_t count,
+                           const pk_segment* segments, int32_t head_dim, void* stream);
 
 /* Bytes of split-K workspace pk_decode_partials needs for this problem: the
  * partials m, l [batch*Hq][splits] and acc [batch*Hq][splits][hd] fp32, each

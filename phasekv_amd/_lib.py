@@ -69,6 +69,7 @@ class PkDecodeProblem(ctypes.Structure):
         ("q", _c_vp), ("q_bstride", _c_i64), ("q_hstride", _c_i64),
         ("segments", ctypes.POINTER(PkSegment)), ("num_segments", _c_i32),
         ("flags", _c_i32),
+        ("table", _c_vp), ("table_count", _c_i32), ("table_bits", _c_i32),
     ]
 
 
@@ -95,6 +96,9 @@ _SIGNATURES = {
     "pk_decode_workspace_size": (ctypes.c_int, [ctypes.POINTER(PkDecodeProblem),
                                                 ctypes.POINTER(ctypes.c_size_t),
                                                 ctypes.POINTER(_c_i32)]),
+    "pk_segment_table_entry_bytes": (ctypes.c_size_t, []),
+    "pk_segment_table_write": (ctypes.c_int, [_c_vp, _c_i32, _c_i32, ctypes.POINTER(PkSegment),
+                                              _c_i32, _c_vp]),
     "pk_decode_partials": (ctypes.c_int, [ctypes.POINTER(PkDecodeProblem), _c_vp,
                                           ctypes.c_size_t, _c_vp]),
     "pk_decode_combine": (ctypes.c_int, [ctypes.POINTER(PkDecodeProblem), _c_vp, _c_vp, _c_vp,

@@ -13,6 +13,9 @@ constexpr int kCombineTarget = 4;            // partials per combine thread the 
 constexpr int kMinChunk = 64;                 // auto chunk lengths are multiples of this
 
 constexpr uint32_t kXcds = 8;                 // accelerator complex dies of an MI355X
+// Launch-internal segment kind: the work items over a device segment table (kd =
+// the table of SegDev entries, length = entries, chunk_len = entries per item).
+constexpr int kSegTable = 8;
 
 // The workgroup's coordinates in an XCD-contiguous order.  The dispatcher hands
 // consecutive workgroups (x fastest, then y, then z) round-robin to the 8 XCDs,

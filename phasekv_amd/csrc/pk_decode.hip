@@ -300,7 +300,17 @@ static int validate_problem(const pk_decode_problem* p) {
   if (hd & (hd - 1)) return fail("head_dim must be a power of two");
   if (hd > kCombineMaxHd) return fail("head_dim above 256 is not supported");
   if (!p->q) return fail("null q");
-  if (p->num_segments <= 0 || !p->segments) return fail("no segments to attend");
+  if (p->table_count < 0) return fail("table_count must be non-negative");
+  if (p->table_count > 0) {
+    if (!p->table) return fail("null segment table");
+    if (p->table_bits != 2 && p->table_bits != 4) return fail("table_bits must be 2 or 4");
+    if (hd != 64 && hd != 128) return fail("a segment table needs head_dim 64 or 128");
+    if (p->flags & PK_FLAG_GENERIC_KERNEL)
+      return fail("a segment table runs on the MFMA kernel only");
+  }
+  if (p->num_segments < 0 || (p->num_segments > 0 && !p->segments) ||
+      (p->num_segments == 0 && p->table_count == 0))
+    return fail("no segments to attend");
   for (int i = 0; i < p->num_segments; ++i) {
     const pk_segment& s = p->segments[i];
     if (s.length <= 0) return fail("segment " + std::to_string(i) + " is empty");
@@ -334,6 +344,9 @@ static int validate_problem(const pk_decode_problem* p) {
 
 struct Plan {
   bool mfma;            // MFMA fast path (else the generic kernel)
+  int tbl_items = 0;    // work items over the device segment table, per row
+  int tbl_per_item = 0; // table entries per work item (kWaves per wave round)
+  int tbl_gbegin = 0;   // partial column of the first table item
   int G, HS, nslab, tile;
   int C;
   int max_kbits, max_vbits;
@@ -486,6 +499,18 @@ static void plan_weighted(const pk_decode_problem* p, int64_t per_bh, Plan& pl) 
   }
 }
 
+// Work items over the device segment table: one segment per wave, kWaves per item.
+static constexpr int kHostWaves = kThreads / 64;
+static void plan_table(const pk_decode_problem* p, int64_t per_bh, Plan& pl) {
+  (void)per_bh;
+  pl.tbl_per_item = kHostWaves;
+  pl.tbl_items = static_cast<int>(cdiv(p->table_count, kHostWaves));
+  pl.tbl_gbegin = pl.C;
+  pl.C += pl.tbl_items;
+  pl.max_kbits = std::max(pl.max_kbits, (int)p->table_bits);
+  pl.max_vbits = std::max(pl.max_vbits, (int)p->table_bits);
+}
+
 static bool weighted_plan(const pk_decode_problem* p) {
   if (env_int("PK_CHUNK_TOKENS", 0) > 0 || env_int("PK_TARGET_WORKGROUPS", 0) > 0) return false;
   const char* v = getenv("PK_WEIGHTED_PLAN");
@@ -554,6 +579,7 @@ static Plan make_plan(const pk_decode_problem* p) {
   }
   if (pl.seg_order.empty())
     for (int i = 0; i < p->num_segments; ++i) pl.seg_order.push_back(i);
+  if (p->table_count > 0) plan_table(p, per_bh, pl);
   const int64_t rows = (int64_t)p->batch * p->num_q_heads;
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   pl.off_m = 0;
@@ -611,17 +637,30 @@ static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
   dp.ws_acc = reinterpret_cast<float*>(ws + pl.off_acc);
   dp.C = pl.C;
   const size_t lds = generic_lds_bytes(pl, p->head_dim);
-  for (int first = 0; first < p->num_segments; first += kMaxSeg) {
-    const int n = std::min(kMaxSeg, p->num_segments - first);
+  // the inline segments, then (if any) the table's work items as one more launch entry
+  const int entries = p->num_segments + (pl.tbl_items > 0 ? 1 : 0);
+  for (int first = 0; first < entries; first += kMaxSeg) {
+    const int n = std::min(kMaxSeg, entries - first);
     int lchunks = 0;
     for (int i = 0; i < n; ++i) {
-      const int si = pl.seg_order[first + i];
       SegDev& d = dp.seg[i];
-      fill_segment(d, p->segments[si]);
-      d.hd_meta = p->head_dim;
-      d.chunk_len = pl.chunk_len[si];
-      d.n_chunks = pl.n_chunks[si];
-      d.gbegin = pl.gbegin[si];
+      if (first + i == p->num_segments) {
+        d = SegDev{};
+        d.kind = kSegTable;
+        d.length = p->table_count;
+        d.chunk_len = pl.tbl_per_item;
+        d.n_chunks = pl.tbl_items;
+        d.gbegin = pl.tbl_gbegin;
+        d.kd = static_cast<const uint8_t*>(p->table);
+        d.hd_meta = p->head_dim;
+      } else {
+        const int si = pl.seg_order[first + i];
+        fill_segment(d, p->segments[si]);
+        d.hd_meta = p->head_dim;
+        d.chunk_len = pl.chunk_len[si];
+        d.n_chunks = pl.n_chunks[si];
+        d.gbegin = pl.gbegin[si];
+      }
       d.lbegin = lchunks;
       lchunks += d.n_chunks;
     }
@@ -651,8 +690,93 @@ extern "C" int pk_decode_workspace_size(const pk_decode_problem* p, size_t* byte
     int rc = validate_problem(p);
     if (rc) return rc;
     Plan pl = make_plan(p);
+    if (p->table_count > 0 && !pl.mfma)
+      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
+                  "128, 32-token K groups, aligned rows)");
     if (bytes) *bytes = pl.bytes;
     if (total_splits) *total_splits = pl.C;
+    return PK_OK;
+  });
+}
+
+// ---------------------------------------------------------------------------
+// device segment table
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kTableBatch = 8;   // entries per write launch (kernel argument block)
+
+struct TableBatch {
+  int n;
+  SegDev seg[kTableBatch];
+};
+
+__global__ void __launch_bounds__(64) table_write_kernel(SegDev* table, TableBatch batch) {
+  static_assert(sizeof(SegDev) % 4 == 0, "entries copy in words");
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(batch.seg);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(table);
+  const int words = batch.n * (int)(sizeof(SegDev) / 4);
+  for (int i = threadIdx.x; i < words; i += 64) dst[i] = src[i];
+}
+
+// The storage the wave-private group pipeline reads (see pk_segment_table_write).
+int table_entry_check(const pk_segment& s, int hd, int i) {
+  const std::string at = "table entry " + std::to_string(i) + ": ";
+  if (s.kind != PK_SEG_KIVI) return fail(at + "only KIVI segments go to a segment table");
+  if (s.length <= 0) return fail(at + "empty segment");
+  if ((s.k_bits != 2 && s.k_bits != 4) || (s.v_bits != 2 && s.v_bits != 4))
+    return fail(at + "K and V widths must be 2 or 4 bits");
+  if (s.splits != 0 || s.split_len != 0) return fail(at + "segments in a table are not split");
+  if (s.k_data_layout != PK_CODES_TOKEN_MAJOR || s.k_meta_layout != PK_META_GROUP_MAJOR)
+    return fail(at + "K must be stored as quantize_pack writes it (token-major codes, "
+                     "group-major scale / min)");
+  if (!(s.k_group == 32 || (s.length <= 32 && s.k_group >= s.length)) || s.v_group != 32)
+    return fail(at + "K groups of 32 (or one group) and V groups of 32 are required");
+  if (!s.k_data || !s.k_scale || !s.k_mins || !s.v_data || !s.v_scale || !s.v_mins)
+    return fail(at + "null K/V pointer");
+  if (!aligned(s.k_data, 16) || s.k_data_bstride % 16 || s.k_data_hstride % 16)
+    return fail(at + "K code rows must be 16-byte aligned");
+  if (!aligned(s.k_scale, 8) || !aligned(s.k_mins, 8) || s.k_meta_bstride % 4 ||
+      s.k_meta_hstride % 4)
+    return fail(at + "K scale / min rows must be 8-byte aligned");
+  if (!aligned(s.v_data, 16) || s.v_data_bstride % 16 || s.v_data_hstride % 16)
+    return fail(at + "V code rows must be 16-byte aligned");
+  const int vma = hd / 32;
+  if (!aligned(s.v_scale, 2 * vma) || !aligned(s.v_mins, 2 * vma) || s.v_meta_bstride % vma ||
+      s.v_meta_hstride % vma)
+    return fail(at + "V scale / min rows misaligned");
+  if ((int64_t)s.length * s.k_bits / 8 >= ((int64_t)1 << 31) / hd) return fail(at + "segment too long");
+  return PK_OK;
+}
+}  // namespace
+
+extern "C" size_t pk_segment_table_entry_bytes(void) { return sizeof(SegDev); }
+
+extern "C" int pk_segment_table_write(void* table, int32_t first, int32_t count,
+                                      const pk_segment* segments, int32_t head_dim,
+                                      void* stream) {
+  return pk::guarded("pk_segment_table_write", [&]() -> int {
+    clear_error();
+    if (!table) return fail("null table");
+    if (first < 0 || count < 0) return fail("first and count must be non-negative");
+    if (count > 0 && !segments) return fail("null segments");
+    if (head_dim != 64 && head_dim != 128) return fail("head_dim must be 64 or 128");
+    for (int i = 0; i < count; ++i) {
+      const int rc = table_entry_check(segments[i], head_dim, i);
+      if (rc) return rc;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    SegDev* dst = static_cast<SegDev*>(table) + first;
+    for (int i0 = 0; i0 < count; i0 += kTableBatch) {
+      TableBatch batch{};
+      batch.n = std::min(kTableBatch, count - i0);
+      for (int i = 0; i < batch.n; ++i) {
+        fill_segment(batch.seg[i], segments[i0 + i]);
+        batch.seg[i].hd_meta = head_dim;
+      }
+      hipLaunchKernelGGL(table_write_kernel, dim3(1), dim3(64), 0, st, dst + i0, batch);
+      const int rc = check_launch("segment_table_write");
+      if (rc) return rc;
+    }
     return PK_OK;
   });
 }
@@ -664,6 +788,9 @@ extern "C" int pk_decode_partials(const pk_decode_problem* p, void* workspace,
     int rc = validate_problem(p);
     if (rc) return rc;
     Plan pl = make_plan(p);
+    if (p->table_count > 0 && !pl.mfma)
+      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
+                  "128, 32-token K groups, aligned rows)");
     if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
     return launch_partials(p, pl, static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
   });
@@ -694,6 +821,9 @@ extern "C" int pk_decode_combine(const pk_decode_problem* p, const void* workspa
     if (!workspace) return fail("null workspace");
     if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
     Plan pl = make_plan(p);
+    if (p->table_count > 0 && !pl.mfma)
+      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
+                  "128, 32-token K groups, aligned rows)");
     const char* ws = static_cast<const char*>(workspace);
     return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
                           reinterpret_cast<const float*>(ws + pl.off_l),
@@ -711,6 +841,9 @@ extern "C" int pk_fused_decode(const pk_decode_problem* p, void* workspace, size
     if (rc) return rc;
     if (!out) return fail("null output");
     Plan pl = make_plan(p);
+    if (p->table_count > 0 && !pl.mfma)
+      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
+                  "128, 32-token K groups, aligned rows)");
     if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
     hipStream_t s = static_cast<hipStream_t>(stream);
     rc = launch_partials(p, pl, static_cast<char*>(workspace), s);
@@ -766,6 +899,9 @@ extern "C" int pk_fused_decode_noalloc(const pk_decode_problem* p, uint16_t* out
     if (rc) return rc;
     if (!out) return fail("null output");
     Plan pl = make_plan(p);
+    if (p->table_count > 0 && !pl.mfma)
+      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
+                  "128, 32-token K groups, aligned rows)");
     if (pl.bytes > (size_t)PK_NOALLOC_SCRATCH_BYTES)
       return fail("the problem needs " + std::to_string(pl.bytes) +
                   " bytes of split-K workspace; pk_fused_decode_noalloc holds " +

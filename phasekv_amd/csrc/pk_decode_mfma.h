@@ -1021,7 +1021,7 @@ __device__ __forceinline__ void kivi_stages(const SegDev& s, const SegOffsets& o
                                             const KivLoad& kl, int t_first, int t_stride, int nst,
                                             int t_end, int wave, int lane, int tid, char* lds,
                                             int stage_bytes, u4_t (&qb)[HD / 32],
-                                            WaveAcc<HD>& acc, float sl2) {
+                                            WaveAcc<HD>& acc, float& sl2) {
   using R = StageRegs<HD, KB, VB>;
   constexpr int D = kivi_depth(KB, VB, MAXB);
   const int t_last = t_end - 1;
@@ -1258,28 +1258,33 @@ constexpr int kPipeMinGroups = 8;
 // group 0 alone first: when every wave of the launch has only a few groups, the
 // first group's latency decides the finish, and the wider first burst of loads
 // delays it (measured on MI355X).
+// The wave takes groups wslot, wslot + wstride, ... of [t_first, t_end): (wave, 4)
+// when the four waves share a chunk, (0, 1) when the wave owns a whole segment of a
+// device table.  Its two buffers start at lds + wave * wbytes (the waves of a table
+// item can hold different widths, so there wbytes covers the widest layout).  norm:
+// normalize q (first segment of the workgroup).
 template <int HD, int KB, int VB>
 __device__ __forceinline__ void kivi_wave_groups(const SegDev& s, const SegOffsets& o,
                                                  const KivLoad& kl, int t_first, int t_end,
-                                                 int wave, int lane, char* lds,
-                                                 u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
-                                                 float sl2) {
+                                                 int wave, int wslot, int wstride, int lane,
+                                                 char* lds, int wbytes, u4_t (&qb)[HD / 32],
+                                                 WaveAcc<HD>& acc, float& sl2, bool norm) {
   using L = GroupLayout<HD, KB, VB>;
   using R = GroupRegs<HD, KB, VB>;
   constexpr int D = (KB + VB <= 4) ? 2 : 1;
   constexpr int CG = HD / 32;
   const int ng = (t_end - t_first + kTile - 1) / kTile;
-  const int n = (ng - wave + kWaves - 1) / kWaves;
+  const int n = (ng - wslot + wstride - 1) / wstride;
   if (n <= 0) return;
   const int t_last = t_end - 1;
-  char* b0 = lds + wave * 2 * L::bytes;
+  char* b0 = lds + wave * wbytes;
   char* b1 = b0 + L::bytes;
   // the ones row of both buffers' V-min block (never overwritten by the groups)
   if (lane < kTile) {
     reinterpret_cast<uint16_t*>(b0 + L::off_vm)[CG * L::vms + lane] = 0x3C00;
     reinterpret_cast<uint16_t*>(b1 + L::off_vm)[CG * L::vms + lane] = 0x3C00;
   }
-  auto tok = [&](int i) { return t_first + kTile * (wave + kWaves * i); };
+  auto tok = [&](int i) { return t_first + kTile * (wslot + wstride * i); };
   auto buf = [&](int i) { return (i & 1) ? b1 : b0; };
   auto load = [&](R& r, int i) { load_group<HD, KB, VB>(r, s, o, kl, tok(i), t_last, lane); };
   // whether the group in buffer 0 / 1 has a large V scale (set when it is stored)
@@ -1300,7 +1305,7 @@ __device__ __forceinline__ void kivi_wave_groups(const SegDev& s, const SegOffse
       load(r0, 0);
 #pragma unroll
       for (int k = 1; k <= D; ++k) load(r[k % D], k);
-      normalize_q<HD>(qb, sl2);
+      if (norm) normalize_q<HD>(qb, sl2);
       store(r0, 0);
       wave_lds_sync();
       QkOut cur = qk(0);
@@ -1353,7 +1358,7 @@ __device__ __forceinline__ void kivi_wave_groups(const SegDev& s, const SegOffse
   R r[D];
   // group 0 goes out alone, then groups 1 .. D
   load(r[0], 0);
-  normalize_q<HD>(qb, sl2);
+  if (norm) normalize_q<HD>(qb, sl2);
   store(r[0], 0);
 #pragma unroll
   for (int k = 1; k <= D; ++k)
@@ -1391,7 +1396,7 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
                                            int t_stride, int nst, int t_end, int wave, int lane,
                                            int tid, char* lds, int stage_bytes,
                                            u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
-                                           float sl2) {
+                                           float& sl2) {
   KivLoad kl;
   kl.row_bytes = ((int64_t)s.length * KB + 7) / 8;
   kl.row_groups = (s.length + s.kgs - 1) / s.kgs;
@@ -1412,7 +1417,8 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
               (t_stride % kStage == 0) && meta8;
   if constexpr (KB <= 4 && VB <= 4) {
     if (kl.kdata_tm && kl.kmeta_gm && kl.row_bytes < ((int64_t)1 << 31) / HD) {
-      kivi_wave_groups<HD, KB, VB>(s, o, kl, t_first, t_end, wave, lane, lds, qb, acc, sl2);
+      kivi_wave_groups<HD, KB, VB>(s, o, kl, t_first, t_end, wave, wave, kWaves, lane, lds,
+                                   2 * GroupLayout<HD, KB, VB>::bytes, qb, acc, sl2, true);
       return;
     }
   }
@@ -1422,6 +1428,80 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
   else
     kivi_stages<HD, KB, VB, MAXB, false>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
                                    stage_bytes, qb, acc, sl2);
+}
+
+// V code position factor of result row e (4 g4 + e of a block): the power of two
+// the PV product of a VB-bit segment carries on that row.
+__device__ __forceinline__ float v_posfactor(int vb, int e) {
+  return (vb == 2) ? (float)(1 << (2 * e)) : (vb == 4) ? ((e & 1) ? 16.f : 1.f) : 1.f;
+}
+
+// The segments of a device segment table (pk_segment_table_write) that one work
+// item covers: entries 4 item .. 4 item + 3 of ts (kind kSegTable: kd = the table,
+// length = entries), entry 4 item + w to wave w.  The wave runs its segment whole
+// through the wave-private group pipeline (the host admits only segments that path
+// reads).  One segment per wave keeps this straight-line code: in a loop over
+// entries the compiler hoists every bit width's invariants and spills.  Returns the
+// V width of the wave's segment (0 if it had none).
+template <int HD, int MAXB>
+__device__ __forceinline__ int table_entry(const SegDev& ts, int item, int b, int kvh, int wave,
+                                           int lane, char* lds, u4_t (&qb)[HD / 32],
+                                           WaveAcc<HD>& acc, float& sl2) {
+  const int e = __builtin_amdgcn_readfirstlane(kWaves * item + wave);
+  if (e >= ts.length) return 0;
+  // only what the wave path reads, with the (batch, kv head) offsets folded into
+  // the pointers: the entry's other fields never occupy registers
+  const SegDev* tp = reinterpret_cast<const SegDev*>(ts.kd) + e;
+  int len = tp->length;
+  if (tp->seq_lens) len = min(len, tp->seq_lens[b]);
+  if (len <= 0) return 0;
+  const int kbits = tp->kbits, vbits = tp->vbits;
+  SegDev s{};
+  s.length = tp->length;
+  s.kbits = kbits;
+  s.vbits = vbits;
+  s.kgs = tp->kgs;
+  s.kd = tp->kd + (b * tp->kd_bs + kvh * tp->kd_hs);
+  s.ks = tp->ks + (b * tp->km_bs + kvh * tp->km_hs);
+  s.km = tp->km + (b * tp->km_bs + kvh * tp->km_hs);
+  s.vd = tp->vd + (b * tp->vd_bs + kvh * tp->vd_hs);
+  s.vs = tp->vs + (b * tp->vm_bs + kvh * tp->vm_hs);
+  s.vm = tp->vm + (b * tp->vm_bs + kvh * tp->vm_hs);
+  const SegOffsets o = {0, 0, 0, 0};
+  // the waves of the item may hold different widths: buffers for the widest layout
+  constexpr int B22 = GroupLayout<HD, 2, 2>::bytes, B24 = GroupLayout<HD, 2, 4>::bytes;
+  constexpr int B42 = GroupLayout<HD, 4, 2>::bytes, B44 = GroupLayout<HD, 4, 4>::bytes;
+  constexpr int B2x = B22 > B24 ? B22 : B24, B4x = B42 > B44 ? B42 : B44;
+  constexpr int WB = 2 * ((MAXB >= 4) ? (B2x > B4x ? B2x : B4x) : B22);
+  KivLoad kl;
+  kl.row_bytes = ((int64_t)s.length * kbits + 7) / 8;
+  kl.row_groups = (s.length + s.kgs - 1) / s.kgs;
+  kl.k_rows = kl.row_bytes;
+  kl.kmode = 16;
+  kl.kdata_tm = true;
+  kl.kmeta_gm = true;
+  kl.gm_elems = false;
+  kl.kmeta4 = false;
+  switch (kbits * 16 + vbits) {
+    case 0x22:
+      kivi_wave_groups<HD, 2, 2>(s, o, kl, 0, len, wave, 0, 1, lane, lds, WB, qb, acc, sl2, true);
+      break;
+    case 0x24:
+      if constexpr (MAXB >= 4)
+        kivi_wave_groups<HD, 2, 4>(s, o, kl, 0, len, wave, 0, 1, lane, lds, WB, qb, acc, sl2, true);
+      break;
+    case 0x42:
+      if constexpr (MAXB >= 4)
+        kivi_wave_groups<HD, 4, 2>(s, o, kl, 0, len, wave, 0, 1, lane, lds, WB, qb, acc, sl2, true);
+      break;
+    case 0x44:
+      if constexpr (MAXB >= 4)
+        kivi_wave_groups<HD, 4, 4>(s, o, kl, 0, len, wave, 0, 1, lane, lds, WB, qb, acc, sl2, true);
+      break;
+    default:
+      return 0;
+  }
+  return vbits;
 }
 
 // Every 64-byte line of the argument block read at once, at entry.  The fields a
@@ -1494,7 +1574,7 @@ decode_mfma_kernel(const DecodeParams p) {
     qb[k] = *reinterpret_cast<const u4_t*>(p.q + (int64_t)b * p.q_bs + (int64_t)(h0 + nq) * p.q_hs +
                                            32 * k + 8 * g4);
 
-  const float sl2 = p.scale * kLog2e;
+  float sl2 = p.scale * kLog2e;
 
   WaveAcc<HD> acc;
 #pragma unroll
@@ -1504,7 +1584,10 @@ decode_mfma_kernel(const DecodeParams p) {
   acc.mx = -INFINITY;
   acc.l = 0.f;
 
-  if (s.kind == PK_SEG_FP16) {
+  int vb_bits = s.vbits;   // the V width the accumulators carry (KIVI)
+  if (s.kind == kSegTable) {
+    vb_bits = table_entry<HD, MAXB>(s, local, b, kvh, wave, lane, lds, qb, acc, sl2);
+  } else if (s.kind == PK_SEG_FP16) {
     const uint16_t* kbase = reinterpret_cast<const uint16_t*>(s.kd) + b * s.kd_bs + kvh * s.kd_hs;
     const uint16_t* vbase = reinterpret_cast<const uint16_t*>(s.vd) + b * s.vd_bs + kvh * s.vd_hs;
     for (int t0 = t_begin + 32 * wave; t0 < t_end; t0 += 32 * kWaves)
@@ -1575,11 +1658,9 @@ decode_mfma_kernel(const DecodeParams p) {
     for (int c = 0; c < CG; ++c) vbf[c] = __shfl(acc.vbl[c], n);
     l_full = __shfl(acc.vbl[CG % 4], 16 * (CG / 4) + n);
     // V code position factor of result row 4 g4 + e
-    const int vb_bits = s.vbits;
     f4_t f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      f[e] = kTwo24 / ((vb_bits == 2) ? (float)(1 << (2 * e)) : (vb_bits == 4) ? ((e & 1) ? 16.f : 1.f) : 1.f);
+    for (int e = 0; e < 4; ++e) f[e] = kTwo24 / v_posfactor(vb_bits, e);
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb)
       *reinterpret_cast<f4_t*>(mo + (wave * 16 + n) * MP + 16 * bb + 4 * g4) =

@@ -152,12 +152,101 @@ def fp16_segment(k: torch.Tensor, v: torch.Tensor, *, batched: bool, splits: int
     return Segment(d, keep, s_len, hkv, hd, batch, dev)
 
 
+# Segments longer than this stay in the launch's own segment list: a table segment is
+# read whole by one wave, which suits the short cold segments of lazy cooling.
+TABLE_MAX_TOKENS = 128
+
+
+def table_eligible(seg: Segment) -> bool:
+    """Whether ``pk_segment_table_write`` takes this segment (see include/phasekv_hip.h):
+    a KIVI segment of 2/4-bit codes in the storage ``quantize_pack`` writes, with aligned
+    rows, at head_dim 64 / 128 and at most ``TABLE_MAX_TOKENS`` tokens."""
+    d = seg.desc
+    if d.kind != _lib.PK_SEG_KIVI or seg.head_dim not in (64, 128):
+        return False
+    if d.k_bits not in (2, 4) or d.v_bits not in (2, 4) or d.splits or d.split_len:
+        return False
+    if d.length > TABLE_MAX_TOKENS:
+        return False
+    if (d.k_data_layout != _lib.PK_CODES_TOKEN_MAJOR
+            or d.k_meta_layout != _lib.PK_META_GROUP_MAJOR):
+        return False
+    if not (d.k_group == 32 or (d.length <= 32 and d.k_group >= d.length)) or d.v_group != 32:
+        return False
+    vma = seg.head_dim // 32
+    return (d.k_data % 16 == 0 and d.k_data_bstride % 16 == 0 and d.k_data_hstride % 16 == 0
+            and d.k_scale % 8 == 0 and d.k_mins % 8 == 0 and d.k_meta_bstride % 4 == 0
+            and d.k_meta_hstride % 4 == 0 and d.v_data % 16 == 0 and d.v_data_bstride % 16 == 0
+            and d.v_data_hstride % 16 == 0 and d.v_scale % (2 * vma) == 0
+            and d.v_mins % (2 * vma) == 0 and d.v_meta_bstride % vma == 0
+            and d.v_meta_hstride % vma == 0)
+
+
+class SegmentTable:
+    """Segment descriptors in device memory (``pk_segment_table_write``), appended to as
+    the cache grows, so that a decode over any number of them is one partials launch.
+
+    The entries are written on the current stream by a small kernel; decode launches
+    ordered after it read them.  ``segments`` keeps the described tensors alive."""
+
+    def __init__(self, device: torch.device, head_dim: int, capacity: int = 64):
+        self.device = device
+        self.head_dim = head_dim
+        self.entry_bytes = int(_lib.load().pk_segment_table_entry_bytes())
+        self.buf = torch.empty(max(1, capacity) * self.entry_bytes, dtype=torch.uint8,
+                               device=device)
+        self.segments: List[Segment] = []
+        self.bits = 0
+
+    @property
+    def count(self) -> int:
+        return len(self.segments)
+
+    def _write(self, first: int, segs: Sequence[Segment]) -> None:
+        if not segs:
+            return
+        arr = (_lib.PkSegment * len(segs))(*[sg.desc for sg in segs])
+        _lib.check(_lib.load().pk_segment_table_write(
+            self.buf.data_ptr(), first, len(segs), arr, self.head_dim,
+            _lib.stream_ptr(self.device)), "segment_table_write")
+
+    def extend(self, segs: Sequence[Segment]) -> None:
+        """Append entries for ``segs`` (each must be ``table_eligible``)."""
+        for sg in segs:
+            if not table_eligible(sg) or sg.head_dim != self.head_dim:
+                raise ValueError("segment not eligible for a device segment table")
+        need = (self.count + len(segs)) * self.entry_bytes
+        if need > self.buf.numel():
+            # a larger table: every entry is written again into it
+            self.buf = torch.empty(max(need, 2 * self.buf.numel()), dtype=torch.uint8,
+                                   device=self.device)
+            self._write(0, self.segments)
+        self._write(self.count, segs)
+        self.segments.extend(segs)
+        for sg in segs:
+            self.bits = max(self.bits, sg.desc.k_bits, sg.desc.v_bits)
+
+
+def split_for_table(segments: List[Segment], candidates: Sequence[bool]):
+    """(inline, table) segments: when the list is longer than one launch's segment list,
+    the eligible candidates (cold segments) go to a device table, the rest stay inline."""
+    if len(segments) <= _lib.PK_MAX_SEGMENTS_PER_LAUNCH:
+        return list(segments), []
+    inline, table = [], []
+    for sg, cand in zip(segments, candidates):
+        (table if cand and table_eligible(sg) else inline).append(sg)
+    if len(table) < 2:
+        return list(segments), []
+    return inline, table
+
+
 class Problem:
-    """A decode problem (q plus segments) as the C structure, with its keep-alive list."""
+    """A decode problem (q, its segment list and an optional device segment table) as the
+    C structure, with its keep-alive list."""
 
     def __init__(self, q: torch.Tensor, segments: List[Segment], num_attention_heads: int,
-                 generic_kernel: bool = False):
-        if not segments:
+                 generic_kernel: bool = False, table: Optional[SegmentTable] = None):
+        if not segments and (table is None or table.count == 0):
             raise ValueError("no KV to attend: every tier is empty")
         if q.dim() == 2:
             q = q.unsqueeze(0)
@@ -169,8 +258,9 @@ class Problem:
         if hq != num_attention_heads:
             raise ValueError(f"query has {hq} heads, expected {num_attention_heads}")
         dev = _lib.require_device(q, *[t for s in segments for t in s.keep])
-        hkv = segments[0].num_kv_heads
-        for s in segments:
+        all_segs = list(segments) + (list(table.segments) if table is not None else [])
+        hkv = all_segs[0].num_kv_heads
+        for s in all_segs:
             if s.num_kv_heads != hkv or s.head_dim != hd:
                 raise ValueError("segments must share kv heads and head_dim with the query")
             if s.batch != batch:
@@ -179,11 +269,14 @@ class Problem:
             raise ValueError(f"Hq {hq} must be a multiple of Hkv {hkv}")
         if q.stride(-1) != 1:
             q = q.contiguous()
+        if table is not None and table.device != dev:
+            raise ValueError("the segment table lives on another device")
         self.q = q
         self.segments = segments
+        self.table = table
         self.device = dev
         self.batch, self.hq, self.hkv, self.hd = batch, hq, hkv, hd
-        arr = (_lib.PkSegment * len(segments))(*[s.desc for s in segments])
+        arr = (_lib.PkSegment * max(1, len(segments)))(*[s.desc for s in segments])
         self._arr = arr
         p = _lib.PkDecodeProblem()
         p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim = batch, hq, hkv, hd
@@ -192,6 +285,10 @@ class Problem:
         p.segments = ctypes.cast(arr, ctypes.POINTER(_lib.PkSegment))
         p.num_segments = len(segments)
         p.flags = _lib.PK_FLAG_GENERIC_KERNEL if generic_kernel else 0
+        if table is not None and table.count:
+            p.table = table.buf.data_ptr()
+            p.table_count = table.count
+            p.table_bits = table.bits
         self.c = p
 
     def workspace_size(self) -> Tuple[int, int]:

@@ -257,10 +257,14 @@ def _reused_problem(q: torch.Tensor, tiers, num_attention_heads: int) -> _dec.Pr
             problem.c.q = q3.data_ptr()
             problem.c.q_bstride, problem.c.q_hstride = q3.stride(0), q3.stride(1)
             if hot is not None:
-                problem._arr[len(segments)].length = hot_len
+                # the hot window is the last segment of the launch's own list
+                problem._arr[len(problem.segments) - 1].length = hot_len
                 problem.segments[-1].length = hot_len
             return problem
-    problem = phasekv_problem(q, tiers, num_attention_heads)
+    # a cooling event appends cold segments: the device table of the kept problem is
+    # extended in place (one small write launch) instead of written again
+    problem = phasekv_problem(q, tiers, num_attention_heads,
+                              reuse_table=kept[3].table if kept is not None else None)
     if hot is not None:
         d = problem.segments[-1].desc
         if d.k_data != hot[0].data_ptr() or d.v_data != hot[1].data_ptr():
@@ -272,12 +276,34 @@ def _reused_problem(q: torch.Tensor, tiers, num_attention_heads: int) -> _dec.Pr
     return problem
 
 
+def _with_table(q: torch.Tensor, segs, candidates, num_attention_heads: int,
+                reuse_table: _dec.SegmentTable | None = None) -> _dec.Problem:
+    """The problem of ``segs``: more segments than one launch's list holds put the eligible
+    candidates (the cold segments) into a device segment table, so the partials stay one
+    launch whatever the number of cold segments.  A ``reuse_table`` whose entries are a
+    prefix of the new table is extended instead of written again."""
+    inline, tsegs = _dec.split_for_table(segs, candidates)
+    table = None
+    if tsegs:
+        if (reuse_table is not None and reuse_table.count <= len(tsegs)
+                and reuse_table.device == q.device
+                and all(a is b for a, b in zip(reuse_table.segments, tsegs))):
+            table = reuse_table
+        else:
+            table = _dec.SegmentTable(q.device, tsegs[0].head_dim, capacity=2 * len(tsegs))
+        table.extend(tsegs[table.count:])
+    return _dec.Problem(q, inline, num_attention_heads, table=table)
+
+
 def phasekv_problem(q: torch.Tensor, tiers, num_attention_heads: int, batched: bool = False,
                     prompt_lens: torch.Tensor | None = None, num_splits: int | None = None,
-                    block_n: int | None = None, num_warps: int | None = None) -> _dec.Problem:
+                    block_n: int | None = None, num_warps: int | None = None,
+                    reuse_table: _dec.SegmentTable | None = None) -> _dec.Problem:
     """The decode problem (every packed segment + the hot window) of one layer's tiers."""
-    segs = []
+    segs, cold = [], []
+    n_first = 1 + len(tiers.prompt_extensions)
     for i, segment in enumerate([tiers.prompt, *tiers.prompt_extensions, *tiers.cold]):
+        cold.append(i >= n_first)
         if batched:
             lens = prompt_lens.to(torch.int32) if (i == 0 and prompt_lens is not None) else None
             segs.append(_dec.packed_segment(segment.key, segment.value, batched=True,
@@ -293,7 +319,8 @@ def phasekv_problem(q: torch.Tensor, tiers, num_attention_heads: int, batched: b
         hot_k, hot_v = tiers.hot_views()
         segs.append(_dec.fp16_segment(hot_k if batched else hot_k[0],
                                       hot_v if batched else hot_v[0], batched=batched))
-    return _dec.Problem(q, segs, num_attention_heads)
+        cold.append(False)
+    return _with_table(q, segs, cold, num_attention_heads, reuse_table)
 
 
 def fused_phasekv_decode(q: torch.Tensor, tiers, num_attention_heads: int,
@@ -362,13 +389,16 @@ def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_h
         raise ValueError("the PhaseKV prompt chunk path takes batch = 1")
     start = hot_len - T
     if method in ("batch", "auto"):
+        packed = [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]
         segs = [_dec.packed_segment(_remove_batch(seg.key), _remove_batch(seg.value),
                                     batched=False, broadcast=T)
-                for seg in [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]]
+                for seg in packed]
+        cold = [i > len(tiers.prompt_extensions) for i in range(len(packed))]
         lens = torch.arange(start + 1, start + T + 1, dtype=torch.int32, device=q.device)
         segs.append(_dec.fp16_segment(hot_k[0], hot_v[0], batched=False, seq_lens=lens,
                                       broadcast=T))
-        return _dec.fused_decode(_dec.Problem(q.contiguous(), segs, hq))
+        cold.append(False)
+        return _dec.fused_decode(_with_table(q.contiguous(), segs, cold, hq))
     # (a) packed tiers and the pre-chunk hot rows, the T queries as heads (kv, g, t)
     segs = []
     for segment in [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]:

@@ -176,6 +176,46 @@ def make_workload(cfg: Config, device, seed: int = 1234, keep_dense: bool = Fals
     return wl
 
 
+def tiers_algorithmic_bytes(tiers: LayerTiers, hq: int) -> int:
+    """Algorithmic bytes of one decode step over ``tiers`` (every packed segment at its own
+    length and width, the hot window, q and the output)."""
+    B, hkv, _, hd = tiers.hot_k.shape
+    total = 0
+    for s in [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]:
+        total += _packed_bytes(s.key.orig_shape[2], hd, s.key.bits) * hkv * B
+    return total + 4 * hd * tiers.hot_len * hkv * B + 2 * 2 * B * hq * hd
+
+
+def make_long_generation(cfg: Config, generated: int, device, seed: int = 1234,
+                         lazy_g: int = 16, keep_ratio: float = 1.0,
+                         window: int = 32) -> Workload:
+    """``cfg``'s batch-1 cache after ``generated`` decode tokens under lazy cooling: the
+    prompt tier, ``cfg``'s cold tier, one cold segment of ``round(lazy_g * keep_ratio)``
+    tokens at ``cfg.cold_bits`` per ``lazy_g`` generated tokens (packed as the cooling
+    launch packs them) and a hot window of ``window`` + 8 tokens."""
+    wl = make_workload(cfg, device, seed=seed)
+    gen = torch.Generator().manual_seed(seed + 7)
+    keep = max(1, round(lazy_g * keep_ratio))
+    B, hkv, hd = cfg.batch, cfg.hkv, cfg.hd
+    n_seg = max(0, generated - window) // lazy_g
+    segs = []
+    for _ in range(n_seg):
+        k = _dense(gen, (B, hkv, keep, hd), cfg.k_kind, seed)
+        v = _dense(gen, (B, hkv, keep, hd), "normal", seed)
+        segs.append(pack_kv(k.to(device), v.to(device), cfg.cold_bits, GROUP))
+    hot = window + 8
+    hot_k = torch.zeros(B, hkv, window + lazy_g, hd, dtype=torch.float16, device=device)
+    hot_v = torch.zeros_like(hot_k)
+    hot_k[:, :, :hot] = _dense(gen, (B, hkv, hot, hd), cfg.k_kind, seed).to(device)
+    hot_v[:, :, :hot] = _dense(gen, (B, hkv, hot, hd), "normal", seed).to(device)
+    tiers = LayerTiers(prompt=wl.tiers.prompt, cold=list(wl.tiers.cold) + segs, hot_k=hot_k,
+                       hot_v=hot_v, hot_len=hot)
+    long_cfg = Config(f"{cfg.name}+{generated}gen", B, cfg.hq, hkv, hd, cfg.prompt,
+                      cfg.prompt_bits, cfg.cold + n_seg * keep, cfg.cold_bits, hot, cfg.k_kind,
+                      cfg.ragged_min)
+    return Workload(long_cfg, wl.q, tiers, wl.prompt_lens, wl.prompt_lens_list)
+
+
 def clone_tiers(t: LayerTiers) -> LayerTiers:
     """Deep copy of the device tensors (for buffer rotation in timing loops)."""
     def cseg(s: PackedKVSegment) -> PackedKVSegment:

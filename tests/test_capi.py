@@ -48,6 +48,7 @@ int main(void) {
   F(pk_segment, seq_lens) F(pk_segment, k_data) F(pk_segment, v_mins)
   F(pk_segment, k_data_bstride) F(pk_segment, tok_stride)
   F(pk_decode_problem, q) F(pk_decode_problem, segments) F(pk_decode_problem, num_segments)
+  F(pk_decode_problem, table) F(pk_decode_problem, table_count) F(pk_decode_problem, table_bits)
   return 0;
 }
 ''')
