@@ -84,6 +84,26 @@ class PackedArrays:
         return int(self.packed.size + 2 * (self.scale.size + self.mins.size))
 
 
+def _group_min_max(xg: np.ndarray):
+    """Per-group ``amin`` / ``amax`` over the last axis (``packing.py:141-142``).
+
+    A left-to-right fold that takes the new element only when it compares
+    strictly smaller (larger) or is NaN.  This fixes the two results IEEE
+    comparison leaves open: a NaN anywhere gives NaN, and among equal values the
+    first one is kept, which decides the sign of a zero min/max when a group
+    holds both +0.0 and -0.0 (torch's CPU reduction over groups this short keeps
+    the first as well).
+    """
+    mn = xg[..., 0:1].copy()
+    mx = mn.copy()
+    for i in range(1, xg.shape[-1]):
+        v = xg[..., i:i + 1]
+        nan = np.isnan(v)
+        mn = np.where((v < mn) | nan, v, mn)
+        mx = np.where((v > mx) | nan, v, mx)
+    return mn, mx
+
+
 def quantize_pack(x: np.ndarray, bits: int, axis: int, group_size) -> PackedArrays:
     """Grouped asymmetric min/max quantization along ``axis`` (``packing.py:115-155``).
 
@@ -109,8 +129,7 @@ def quantize_pack(x: np.ndarray, bits: int, axis: int, group_size) -> PackedArra
     padded = xf.shape[-1]
     n_groups = padded // gs
     xg = xf.reshape(xf.shape[:-1] + (n_groups, gs))
-    g_min = xg.min(axis=-1, keepdims=True)
-    g_max = xg.max(axis=-1, keepdims=True)
+    g_min, g_max = _group_min_max(xg)
     scale = np.maximum(g_max - g_min, np.float32(1e-8)).astype(np.float32) / np.float32(qmax)
     scale = scale.astype(np.float32)
     q = np.rint((xg - g_min) / scale).astype(np.float32)

@@ -52,6 +52,20 @@ def constructed_inputs():
     heavy[..., 5] *= 40
     heavy[..., 17] *= -25
     cases["outliers"] = heavy.to(torch.float16).numpy()
+    # IEEE specials: groups holding a NaN, +inf, -inf, both infinities, signed zeros only,
+    # and a NaN beside an infinity, next to ordinary groups (how amin / amax, the scale's
+    # clamp, round and the uint8 cast treat them fixes codes, scales and mins)
+    sp = torch.randn(1, 2, 40, 8, generator=g)
+    sp[0, 0, 3, 1] = float("nan")
+    sp[0, 0, 12, 2] = float("inf")
+    sp[0, 1, 20, 3] = float("-inf")
+    sp[0, 1, 33, 4] = float("inf")
+    sp[0, 1, 34, 4] = float("-inf")
+    sp[0, 0, 32:40, 5] = 0.0
+    sp[0, 0, 32:40:2, 5] = -0.0
+    sp[0, 1, 6, 6] = float("nan")
+    sp[0, 1, 7, 6] = float("inf")
+    cases["specials"] = sp.to(torch.float16).numpy()
     return cases
 
 

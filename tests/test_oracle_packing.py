@@ -4,7 +4,7 @@ The oracle restates src/phasekv/kernels/packing.py; these checks do not retype
 its formulas: the golden vectors come from the reference module itself, the
 brute-force checks build bytes bit by bit, and the planted-mistake checks show
 that each plausible slip (fp16 scale for codes, rounding mode, bit order,
-bit order) fails at least one golden vector.
+a min/max that skips NaN) fails at least one golden vector.
 """
 import numpy as np
 import pytest
@@ -21,7 +21,7 @@ def golden():
 def _quant_matches(pt, z, key):
     return (np.array_equal(pt.packed, z[key + "_packed"])
             and np.array_equal(pt.scale.view(np.uint16), z[key + "_scale"].view(np.uint16))
-            and np.array_equal(pt.mins.view(np.uint16), z[key + "_mins"].view(np.uint16)))
+            and golden_data.same_min_bits(pt.mins, z[key + "_mins"]))
 
 
 def test_oracle_quantize_matches_reference_golden(golden):
@@ -128,8 +128,13 @@ def _mutant_quantize(x, bits, axis, group_size, mutation):
     if pad:
         xf = np.concatenate([xf, np.broadcast_to(xf[..., -1:], xf.shape[:-1] + (pad,))], -1)
     xg = xf.reshape(xf.shape[:-1] + (xf.shape[-1] // gs, gs))
-    mn = xg.min(-1, keepdims=True)
-    mx = xg.max(-1, keepdims=True)
+    if mutation == "nan_skipping":
+        with np.errstate(invalid="ignore"):
+            mn = np.fmin.reduce(xg, axis=-1, keepdims=True)
+            mx = np.fmax.reduce(xg, axis=-1, keepdims=True)
+    else:
+        mn = xg.min(-1, keepdims=True)
+        mx = xg.max(-1, keepdims=True)
     scale = (np.maximum(mx - mn, np.float32(1e-8)) / np.float32(qmax)).astype(np.float32)
     use = scale
     if mutation == "fp16_scale":
@@ -154,7 +159,7 @@ def _mutant_quantize(x, bits, axis, group_size, mutation):
     return packed, scale[..., 0].astype(np.float16), mn[..., 0].astype(np.float16)
 
 
-@pytest.mark.parametrize("mutation", ["fp16_scale", "round_half_up", "msb_first"])
+@pytest.mark.parametrize("mutation", ["fp16_scale", "round_half_up", "msb_first", "nan_skipping"])
 def test_planted_quantize_mistakes_fail_golden(golden, mutation):
     z, man = golden
     failures = 0
@@ -164,7 +169,8 @@ def test_planted_quantize_mistakes_fail_golden(golden, mutation):
                                                case["group_size"], mutation)
         k = case["key"]
         if not (np.array_equal(packed, z[k + "_packed"])
-                and np.array_equal(scale.view(np.uint16), z[k + "_scale"].view(np.uint16))):
+                and np.array_equal(scale.view(np.uint16), z[k + "_scale"].view(np.uint16))
+                and golden_data.same_min_bits(mins, z[k + "_mins"])):
             failures += 1
     assert failures > 0, f"golden vectors do not detect the '{mutation}' mistake"
 
