@@ -165,6 +165,7 @@ typedef struct pk_decode_problem {
 } pk_decode_problem;
 
 #define PK_FLAG_GENERIC_KERNEL 1   /* use the general-shape kernel even where the MFMA one applies */
+#define PK_FLAG_REQUIRE_MFMA 2     /* fail (PK_ERR_INVALID) where the MFMA kernel does not apply */
 
 /* ---- device-resident segment table ------------------------------------------
  * The cache's packed segments as descriptors in device memory, so that a decode

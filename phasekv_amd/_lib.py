@@ -29,6 +29,7 @@ PK_SEG_FP16 = 2
 PK_MAX_SEGMENTS_PER_LAUNCH = 8
 PK_NOALLOC_SCRATCH_BYTES = 16 << 20
 PK_FLAG_GENERIC_KERNEL = 1
+PK_FLAG_REQUIRE_MFMA = 2
 
 PK_META_CHANNEL_MAJOR = 0
 PK_META_GROUP_MAJOR = 1

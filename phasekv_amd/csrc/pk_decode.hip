@@ -359,13 +359,22 @@ struct Plan {
 static bool aligned(const void* ptr, int64_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
 
 // The MFMA kernel covers head_dim 64 / 128, FP16 segments with 16-byte aligned
-// rows and KIVI segments with 32-token K groups (or a single group) and 32-channel
-// V groups; explicit split lengths must be whole 32-token groups.
+// rows, KIVI segments with 32-token K groups (or a single group) and 32-channel
+// V groups, and per-token K segments with 32-channel K and V groups (not in the
+// same launch as KIVI segments); explicit split lengths must be whole 32-token
+// groups.
 static bool mfma_eligible(const pk_decode_problem* p) {
   if (p->flags & PK_FLAG_GENERIC_KERNEL) return false;
   const int hd = p->head_dim;
   if (hd != 64 && hd != 128) return false;
   if (!aligned(p->q, 16) || p->q_hstride % 8 || p->q_bstride % 8) return false;
+  bool has_kivi = p->table_count > 0, has_token = false;
+  for (int i = 0; i < p->num_segments; ++i) {
+    has_kivi = has_kivi || p->segments[i].kind == PK_SEG_KIVI;
+    has_token = has_token || p->segments[i].kind == PK_SEG_TOKEN;
+  }
+  if (has_kivi && has_token) return false;
+  const int ns = hd / 32;
   for (int i = 0; i < p->num_segments; ++i) {
     const pk_segment& s = p->segments[i];
     if (s.splits > 0) {
@@ -381,13 +390,24 @@ static bool mfma_eligible(const pk_decode_problem* p) {
         return false;
       continue;
     }
-    if (s.kind != PK_SEG_KIVI) return false;
+    if (s.kind == PK_SEG_TOKEN) {
+      // K code rows (hd * k_bits / 8 bytes) in 16-byte pieces, K metadata one token
+      // (hd / 32 fp16) per load
+      if (s.k_group != 32 || s.v_group != 32) return false;
+      if (!aligned(s.k_data, 16) || s.k_data_bstride % 16 || s.k_data_hstride % 16) return false;
+      if (!aligned(s.k_scale, 2 * ns) || !aligned(s.k_mins, 2 * ns) || s.k_meta_bstride % ns ||
+          s.k_meta_hstride % ns)
+        return false;
+    } else if (s.kind != PK_SEG_KIVI) {
+      return false;
+    }
     // token-major K codes are read in 16-byte pieces of HD-byte rows
     if (s.k_data_layout == PK_CODES_TOKEN_MAJOR &&
         (!aligned(s.k_data, 16) || s.k_data_bstride % 16 || s.k_data_hstride % 16))
       return false;
     // K groups of 32 tokens, or one group for a segment of at most 32 tokens
-    if (!(s.k_group == 32 || (s.length <= 32 && s.k_group >= s.length)) || s.v_group != 32)
+    if (s.kind == PK_SEG_KIVI &&
+        (!(s.k_group == 32 || (s.length <= 32 && s.k_group >= s.length)) || s.v_group != 32))
       return false;
     // K rows and K metadata are read at whatever alignment they have; V rows in
     // 16-byte pieces and V metadata one token (hd / 32 fp16) per load
@@ -589,6 +609,20 @@ static Plan make_plan(const pk_decode_problem* p) {
   return pl;
 }
 
+// Requirements of the problem on the kernel choice: a device table and
+// PK_FLAG_REQUIRE_MFMA need the MFMA kernel.
+static int check_plan(const pk_decode_problem* p, const Plan& pl) {
+  if (pl.mfma) return PK_OK;
+  if (p->table_count > 0)
+    return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
+                "128, 32-token K groups, aligned rows)");
+  if (p->flags & PK_FLAG_REQUIRE_MFMA)
+    return fail("the MFMA kernel does not apply (head_dim 64 / 128, 32-token K groups or "
+                "32-channel groups, aligned rows, whole 32-token splits, no KIVI and per-token "
+                "K segments together)");
+  return PK_OK;
+}
+
 static void fill_segment(SegDev& d, const pk_segment& s) {
   d.kind = s.kind;
   d.length = s.length;
@@ -690,9 +724,7 @@ extern "C" int pk_decode_workspace_size(const pk_decode_problem* p, size_t* byte
     int rc = validate_problem(p);
     if (rc) return rc;
     Plan pl = make_plan(p);
-    if (p->table_count > 0 && !pl.mfma)
-      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
-                  "128, 32-token K groups, aligned rows)");
+    if (int rc = check_plan(p, pl)) return rc;
     if (bytes) *bytes = pl.bytes;
     if (total_splits) *total_splits = pl.C;
     return PK_OK;
@@ -788,9 +820,7 @@ extern "C" int pk_decode_partials(const pk_decode_problem* p, void* workspace,
     int rc = validate_problem(p);
     if (rc) return rc;
     Plan pl = make_plan(p);
-    if (p->table_count > 0 && !pl.mfma)
-      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
-                  "128, 32-token K groups, aligned rows)");
+    if (int rc = check_plan(p, pl)) return rc;
     if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
     return launch_partials(p, pl, static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
   });
@@ -821,9 +851,7 @@ extern "C" int pk_decode_combine(const pk_decode_problem* p, const void* workspa
     if (!workspace) return fail("null workspace");
     if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
     Plan pl = make_plan(p);
-    if (p->table_count > 0 && !pl.mfma)
-      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
-                  "128, 32-token K groups, aligned rows)");
+    if (int rc = check_plan(p, pl)) return rc;
     const char* ws = static_cast<const char*>(workspace);
     return launch_combine(reinterpret_cast<const float*>(ws + pl.off_m),
                           reinterpret_cast<const float*>(ws + pl.off_l),
@@ -841,9 +869,7 @@ extern "C" int pk_fused_decode(const pk_decode_problem* p, void* workspace, size
     if (rc) return rc;
     if (!out) return fail("null output");
     Plan pl = make_plan(p);
-    if (p->table_count > 0 && !pl.mfma)
-      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
-                  "128, 32-token K groups, aligned rows)");
+    if (int rc = check_plan(p, pl)) return rc;
     if (!workspace || workspace_bytes < pl.bytes) return fail("workspace too small");
     hipStream_t s = static_cast<hipStream_t>(stream);
     rc = launch_partials(p, pl, static_cast<char*>(workspace), s);
@@ -899,9 +925,7 @@ extern "C" int pk_fused_decode_noalloc(const pk_decode_problem* p, uint16_t* out
     if (rc) return rc;
     if (!out) return fail("null output");
     Plan pl = make_plan(p);
-    if (p->table_count > 0 && !pl.mfma)
-      return fail("a segment table needs every other segment on the MFMA path (head_dim 64 / "
-                  "128, 32-token K groups, aligned rows)");
+    if (int rc = check_plan(p, pl)) return rc;
     if (pl.bytes > (size_t)PK_NOALLOC_SCRATCH_BYTES)
       return fail("the problem needs " + std::to_string(pl.bytes) +
                   " bytes of split-K workspace; pk_fused_decode_noalloc holds " +

@@ -186,7 +186,9 @@ __device__ __forceinline__ uint32_t hmax4(u2_t x) {
 // The workgroup's q normalization exponent e: the smallest e >= 0 with every |q| of
 // the lane's registers and of the wave (every wave holds all heads of the
 // workgroup) at most 2^e.
-template <int KS>
+// UP: also negative e, the smallest e with every |q| at most 2^e (largest |q'| in
+// (1/2, 1]; e >= -15 for any fp16 q).
+template <int KS, bool UP = false>
 __device__ __forceinline__ int q_norm_shift(const u4_t (&qb)[KS]) {
   uint32_t m = 0;
 #pragma unroll
@@ -209,14 +211,14 @@ __device__ __forceinline__ int q_norm_shift(const u4_t (&qb)[KS]) {
   // inf / NaN: the largest finite exponent (the result is not finite anyway)
   m = __builtin_amdgcn_readfirstlane(min(m, 0x7BFFu));
   const int e = (int)(m >> 10) - 15 + ((m & 0x3ffu) ? 1 : 0);
-  return e > 0 ? e : 0;
+  return (UP || e > 0) ? e : 0;
 }
 
 // q' = q * 2^-e (|q'| <= 1) and sl2 * 2^e: the K fold q' * sK stays in fp16.  Called
 // by the KIVI paths after their first group's loads are issued (it waits for q).
-template <int HD>
+template <int HD, bool UP = false>
 __device__ __forceinline__ void normalize_q(u4_t (&qb)[HD / 32], float& sl2) {
-  const int e = q_norm_shift<HD / 32>(qb);
+  const int e = q_norm_shift<HD / 32, UP>(qb);
   const uint32_t f = pack_h2(ldexpf(1.f, -e), ldexpf(1.f, -e));
 #pragma unroll
   for (int k = 0; k < HD / 32; ++k)
@@ -1130,15 +1132,90 @@ struct GroupLayout {
   __device__ static constexpr int vswz(int s, int b) { return 8 * ((s ^ (b >> 1)) & 1); }
 };
 
+// ---------------------------------------------------------------------------
+// The V side of a wave-private 32-token group (V per token, 32-channel groups),
+// shared by the KIVI and the per-token K groups.  VB = 2, 4: the spread layout of
+// StageLayout (items (token pair, PW-word slice), slice fastest); every lane
+// loads unconditionally, rows clamped to t_last.
+// ---------------------------------------------------------------------------
+template <int HD, int VB>
+struct VGroupShape {
+  static constexpr int W = HD * VB / 32;        // words per V row
+  static constexpr int PW = (W >= 16) ? 4 : 2;
+  static constexpr int NQ = W / PW;
+  static constexpr int VI = 16 * NQ;            // V items (token pair, slice) of a group
+};
+
+// t0: wave-uniform first token of the group
+template <int HD, int VB>
+__device__ __forceinline__ void load_group_vcodes(u4_t& va, u4_t& vb, const SegDev& s,
+                                                  const SegOffsets& o, int t0, int t_last,
+                                                  int lane) {
+  using V = VGroupShape<HD, VB>;
+  constexpr int RB = HD * VB / 8;
+  const int q = lane % V::VI;
+  const uint32_t tp = q / V::NQ, qw = q - tp * V::NQ;
+  const uint32_t dt = (uint32_t)(t_last - t0);
+  const uint8_t* vrow = s.vd + o.vd + (int64_t)t0 * RB;
+  const uint8_t* pa = vrow + (min(2u * tp, dt) * RB + qw * V::PW * 4);
+  const uint8_t* pb = vrow + (min(2u * tp + 1u, dt) * RB + qw * V::PW * 4);
+  if constexpr (V::PW == 4) {
+    va = *reinterpret_cast<const u4_t*>(pa);
+    vb = *reinterpret_cast<const u4_t*>(pb);
+  } else {
+    const u2_t a = *reinterpret_cast<const u2_t*>(pa);
+    const u2_t b = *reinterpret_cast<const u2_t*>(pb);
+    va = u4_t{a[0], a[1], 0u, 0u};
+    vb = u4_t{b[0], b[1], 0u, 0u};
+  }
+}
+
+// V scales (lanes < 32) or mins (lanes >= 32) of token lane % 32 (HD = 64: low word only)
+template <int HD>
+__device__ __forceinline__ void load_group_vmeta(u2_t& vm, const SegDev& s, const SegOffsets& o,
+                                                 int t0, int t_last, int lane) {
+  const uint32_t dt = min((uint32_t)(lane & (kTile - 1)), (uint32_t)(t_last - t0));
+  const uint16_t* m = pick(lane < kTile, s.vs, s.vm) + (o.vm + (int64_t)t0 * (HD / 32)) + dt * (HD / 32);
+  if (HD == 128) vm = *reinterpret_cast<const u2_t*>(m);
+  else vm = u2_t{*reinterpret_cast<const uint32_t*>(m), 0u};
+}
+
+template <int HD, int VB, typename L>
+__device__ __forceinline__ void store_group_vcodes(const u4_t& va, const u4_t& vb, int lane, char* st) {
+  using V = VGroupShape<HD, VB>;
+  if (V::VI == 64 || lane < V::VI) {
+    // the store order of StageLayout: 32 stores of a half wave in 32 banks
+    const int tp = lane / V::NQ, qw = lane - tp * V::NQ;
+    const int flip = ((V::NQ == 4) ? (qw >> 1) : qw) & 1;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(st + L::off_vw) + qw * 64;
+#pragma unroll
+    for (int k = 0; k < V::PW; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int b = j ^ flip;
+        const int sw = 8 * ((qw ^ (j >> 1)) & 1);
+        dst[k * V::NQ * 64 + b * 16 + (tp ^ sw)] = perm(vb[k], va[k], sel_bytes(b));
+      }
+  }
+}
+
+// Returns whether a V scale of the group is above kVScaleSafe.
+template <int HD, typename L>
+__device__ __forceinline__ bool store_group_vmeta(const u2_t& vm, int lane, char* st) {
+  uint16_t* m = reinterpret_cast<uint16_t*>(st + ((lane < kTile) ? L::off_vs : L::off_vm));
+  const int t = lane & (kTile - 1);
+#pragma unroll
+  for (int cg = 0; cg < HD / 32; ++cg)
+    m[cg * L::vms + t] = (uint16_t)(vm[cg >> 1] >> (16 * (cg & 1)));
+  // lanes < 32 hold one token's V scales
+  return __ballot(vscale_big(lane < kTile, vm)) != 0;
+}
+
 // One lane's share of a group's loads (64 lanes).
 template <int HD, int KB, int VB>
 struct GroupRegs {
   static constexpr int KP = 4 * KB * HD / 16;   // 16-byte K pieces (4 KB byte rows of HD)
   static constexpr int NK = (KP + 63) / 64;
-  static constexpr int W = HD * VB / 32;        // words per V row
-  static constexpr int PW = (W >= 16) ? 4 : 2;
-  static constexpr int NQ = W / PW;
-  static constexpr int VI = 16 * NQ;            // V items (token pair, slice) of a group
   u4_t k[NK];
   u4_t va, vb;
   u2_t km;     // lanes < HD / 2: 4 channels of the group's K scales (lane < HD / 4) or mins
@@ -1170,30 +1247,8 @@ __device__ __forceinline__ void load_group(GroupRegs<HD, KB, VB>& r, const SegDe
     const uint16_t* m = pick(q < QL, s.ks, s.km) + mrow + 4 * (q & (QL - 1));
     r.km = *reinterpret_cast<const u2_t*>(m);
   }
-  {
-    constexpr int RB = HD * VB / 8;
-    const int q = lane % R::VI;
-    const uint32_t tp = q / R::NQ, qw = q - tp * R::NQ;
-    const uint32_t dt = (uint32_t)(t_last - t0);
-    const uint8_t* vrow = s.vd + o.vd + (int64_t)t0 * RB;
-    const uint8_t* pa = vrow + (min(2u * tp, dt) * RB + qw * R::PW * 4);
-    const uint8_t* pb = vrow + (min(2u * tp + 1u, dt) * RB + qw * R::PW * 4);
-    if constexpr (R::PW == 4) {
-      r.va = *reinterpret_cast<const u4_t*>(pa);
-      r.vb = *reinterpret_cast<const u4_t*>(pb);
-    } else {
-      const u2_t a = *reinterpret_cast<const u2_t*>(pa);
-      const u2_t b = *reinterpret_cast<const u2_t*>(pb);
-      r.va = u4_t{a[0], a[1], 0u, 0u};
-      r.vb = u4_t{b[0], b[1], 0u, 0u};
-    }
-  }
-  {
-    const uint32_t dt = min((uint32_t)(lane & (kTile - 1)), (uint32_t)(t_last - t0));
-    const uint16_t* m = pick(lane < kTile, s.vs, s.vm) + (o.vm + (int64_t)t0 * (HD / 32)) + dt * (HD / 32);
-    if (HD == 128) r.vm = *reinterpret_cast<const u2_t*>(m);
-    else r.vm = u2_t{*reinterpret_cast<const uint32_t*>(m), 0u};
-  }
+  load_group_vcodes<HD, VB>(r.va, r.vb, s, o, t0, t_last, lane);
+  load_group_vmeta<HD>(r.vm, s, o, t0, t_last, lane);
 }
 
 // The group's registers into the wave's buffer (GroupLayout).
@@ -1218,29 +1273,8 @@ __device__ __forceinline__ bool store_group(const GroupRegs<HD, KB, VB>& r, int 
       *reinterpret_cast<u2_t*>(m + 4 * (lane & (QL - 1))) = r.km;
     }
   }
-  if (R::VI == 64 || lane < R::VI) {
-    // the store order of StageLayout: 32 stores of a half wave in 32 banks
-    const int tp = lane / R::NQ, qw = lane - tp * R::NQ;
-    const int flip = ((R::NQ == 4) ? (qw >> 1) : qw) & 1;
-    uint32_t* dst = reinterpret_cast<uint32_t*>(st + L::off_vw) + qw * 64;
-#pragma unroll
-    for (int k = 0; k < R::PW; ++k)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int b = j ^ flip;
-        const int sw = 8 * ((qw ^ (j >> 1)) & 1);
-        dst[k * R::NQ * 64 + b * 16 + (tp ^ sw)] = perm(r.vb[k], r.va[k], sel_bytes(b));
-      }
-  }
-  {
-    uint16_t* m = reinterpret_cast<uint16_t*>(st + ((lane < kTile) ? L::off_vs : L::off_vm));
-    const int t = lane & (kTile - 1);
-#pragma unroll
-    for (int cg = 0; cg < HD / 32; ++cg)
-      m[cg * L::vms + t] = (uint16_t)(r.vm[cg >> 1] >> (16 * (cg & 1)));
-  }
-  // lanes < 32 hold one token's V scales
-  return __ballot(vscale_big(lane < kTile, r.vm)) != 0;
+  store_group_vcodes<HD, VB, L>(r.va, r.vb, lane, st);
+  return store_group_vmeta<HD, L>(r.vm, lane, st);
 }
 
 // Waves with at least this many groups of a two-register-set (2-bit K and V)
@@ -1430,6 +1464,342 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
                                    stage_bytes, qb, acc, sl2);
 }
 
+// ---------------------------------------------------------------------------
+// Per-token K groups (PK_SEG_TOKEN: the reference's legacy layout,
+// src/phasekv/kernels/attention_triton.py:145-282).  K is packed along head_dim
+// like V, with one scale / min per (token, 32-channel group g):
+//   S^T[t][h] = sum_g sK[t][g] * D_g[t][h] + sum_g mK[t][g] * Q_g[h],
+//   D_g[t][h] = sum_{c in g} code_K[t][c] * q[h][c],   Q_g[h] = sum_{c in g} q[h][c].
+// One MFMA per (16 tokens, group) gives D_g in fp32 and the per-token scale and
+// min act on the fp32 results: no fp16 fold, the scores keep fp32 precision.
+// A K code byte holds channels, so the codes of one operand sit at different bit
+// positions (the fp16 subnormal code * 2^(pos - 24)); each channel's factor
+// 2^-pos is folded into the q operand once per segment (exact powers of two, q
+// normalized so that its largest element is in (1/2, 1]).
+//
+// LDS of one group (the wave's buffer):
+//   Kc  [32 tokens][lane group g4][group g][KB bytes]: the KB-byte unit of channels
+//       32 g + 8 g4 .. + 7, so one read gives a lane its token's operands of every
+//       group (the store transposes the row as loaded)
+//   Km  [32 tokens][sK of the HD/32 groups | mK of the HD/32 groups] fp16
+//   V, Vs, Vm as GroupLayout; VB = 8: the rows as stored, StageLayout's pitch
+// Results come in the token order of 8-bit KIVI K (row r of instance h = token
+// 16 h + r), which kivi_softmax_pv<.., KB = 8, ..> follows.
+// ---------------------------------------------------------------------------
+template <int HD, int KB, int VB>
+struct TokLayout {
+  static constexpr int NS = HD / 32;                      // channel groups
+  static constexpr int krow = HD * KB / 8;                // code bytes per token
+  static constexpr int kunits = NS * KB;                  // code bytes a lane reads per token
+  // padded so that the 16 token rows of one operand read spread over the banks
+  static constexpr int kpitch = krow + ((kunits >= 16) ? 16 : 8);
+  static constexpr int kmeta_row = 4 * NS;
+  static constexpr int off_kmeta = kTile * kpitch;
+  static constexpr int off_vw = off_kmeta + kTile * kmeta_row;
+  static constexpr int vrow_words = HD * VB / 32;
+  static constexpr int vrow_bytes = HD * VB / 8;
+  static constexpr bool vspread = VB != 8;
+  static constexpr int vpw = (vrow_words >= 16) ? 4 : 2;
+  static constexpr int vnq = vrow_words / vpw;
+  static constexpr int vgrp_words = vrow_words * 64;
+  static constexpr int vrow_pitch = vrow_bytes + 16;
+  static constexpr int vw_bytes = vspread ? vgrp_words * 4 : kTile * vrow_pitch;
+  static constexpr int vms = kTile + 8;
+  static constexpr int off_vs = off_vw + vw_bytes;
+  static constexpr int off_vm = off_vs + NS * vms * 2;
+  static constexpr int bytes = (off_vm + (NS + 1) * vms * 2 + 15) & ~15;
+  __device__ static constexpr int vslot(int w) { return (w % vpw) * vnq + w / vpw; }
+  __device__ static constexpr int vswz(int s, int b) { return 8 * ((s ^ (b >> 1)) & 1); }
+};
+
+// One lane's share of a per-token group's loads (64 lanes).
+template <int HD, int KB, int VB>
+struct TokRegs {
+  static constexpr int KP = kTile * HD * KB / 128;        // 16-byte K pieces
+  static constexpr int NK = (KP + 63) / 64;
+  static constexpr int VP = kTile * HD / 16;              // 16-byte V pieces at 8 bits
+  static constexpr int NV = (VB == 8) ? (VP + 63) / 64 : 1;
+  u4_t k[NK];
+  u2_t km;         // sK (lanes < 32) or mK (lanes >= 32) of token lane % 32 (HD = 64: low word)
+  u4_t va, vb;     // VB = 2, 4
+  u4_t v[NV];      // VB = 8
+  u2_t vm;
+};
+
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void load_tok_group(TokRegs<HD, KB, VB>& r, const SegDev& s,
+                                               const SegOffsets& o, int t0_, int t_last, int lane) {
+  using R = TokRegs<HD, KB, VB>;
+  constexpr int NS = HD / 32;
+  constexpr int KR = HD * KB / 8;       // code bytes per token
+  constexpr int PR = KR / 16;           // 16-byte pieces per token
+  const int t0 = __builtin_amdgcn_readfirstlane(t0_);
+  const uint32_t dt = (uint32_t)(t_last - t0);
+  const uint8_t* kbase = s.kd + o.kd + (int64_t)t0 * KR;
+#pragma unroll
+  for (int i = 0; i < R::NK; ++i) {
+    const uint32_t q = min((uint32_t)(lane + 64 * i), (uint32_t)R::KP - 1u);
+    r.k[i] = *reinterpret_cast<const u4_t*>(kbase + min(q / PR, dt) * KR + 16u * (q % PR));
+  }
+  {
+    const uint32_t tq = min((uint32_t)(lane & (kTile - 1)), dt);
+    const uint16_t* m = pick(lane < kTile, s.ks, s.km) + (o.km + (int64_t)t0 * NS) + tq * NS;
+    if (HD == 128) r.km = *reinterpret_cast<const u2_t*>(m);
+    else r.km = u2_t{*reinterpret_cast<const uint32_t*>(m), 0u};
+  }
+  if constexpr (VB == 8) {
+    constexpr int PV = HD / 16;
+    const uint8_t* vbase = s.vd + o.vd + (int64_t)t0 * HD;
+#pragma unroll
+    for (int i = 0; i < R::NV; ++i) {
+      const uint32_t q = min((uint32_t)(lane + 64 * i), (uint32_t)R::VP - 1u);
+      r.v[i] = *reinterpret_cast<const u4_t*>(vbase + min(q / PV, dt) * HD + 16u * (q % PV));
+    }
+  } else {
+    load_group_vcodes<HD, VB>(r.va, r.vb, s, o, t0, t_last, lane);
+  }
+  load_group_vmeta<HD>(r.vm, s, o, t0, t_last, lane);
+}
+
+// The group's registers into the wave's buffer (TokLayout).  Returns whether a V
+// scale of the group is above kVScaleSafe.
+template <int HD, int KB, int VB>
+__device__ __forceinline__ bool store_tok_group(const TokRegs<HD, KB, VB>& r, int lane, char* st) {
+  using L = TokLayout<HD, KB, VB>;
+  using R = TokRegs<HD, KB, VB>;
+  constexpr int NS = HD / 32;
+  constexpr int PR = L::krow / 16;
+#pragma unroll
+  for (int i = 0; i < R::NK; ++i) {
+    const int q = lane + 64 * i;
+    if (R::KP % 64 == 0 || q < R::KP) {
+      const int p = q % PR;
+      char* row = st + (q / PR) * L::kpitch;
+      const u4_t w = r.k[i];
+      if constexpr (KB == 2) {
+        // the piece holds groups 2 p and 2 p + 1; unit (g, g4) = bytes 2 g4, 2 g4 + 1 of
+        // the group's 8 bytes.  Units (2 p, g4) and (2 p + 1, g4) are neighbours.
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4)
+          *reinterpret_cast<uint32_t*>(row + 2 * (g4 * NS + 2 * p)) =
+              perm(w[2 + (g4 >> 1)], w[g4 >> 1], sel_halves(g4 & 1));
+      } else if constexpr (KB == 4) {
+        // the piece is group p; unit (p, g4) = word g4
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) *reinterpret_cast<uint32_t*>(row + 4 * (g4 * NS + p)) = w[g4];
+      } else {
+        // the piece is half p % 2 of group p / 2: units g4 = 2 (p % 2) and 2 (p % 2) + 1
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          *reinterpret_cast<u2_t*>(row + 8 * ((2 * (p & 1) + u) * NS + (p >> 1))) =
+              u2_t{w[2 * u], w[2 * u + 1]};
+      }
+    }
+  }
+  {
+    char* m = st + L::off_kmeta + (lane & (kTile - 1)) * L::kmeta_row + ((lane < kTile) ? 0 : 2 * NS);
+    if (HD == 128) *reinterpret_cast<u2_t*>(m) = r.km;
+    else *reinterpret_cast<uint32_t*>(m) = r.km[0];
+  }
+  if constexpr (VB == 8) {
+    constexpr int PV = HD / 16;
+#pragma unroll
+    for (int i = 0; i < R::NV; ++i) {
+      const int q = lane + 64 * i;
+      if (R::VP % 64 == 0 || q < R::VP)
+        *reinterpret_cast<u4_t*>(st + L::off_vw + (q / PV) * L::vrow_pitch + (q % PV) * 16) = r.v[i];
+    }
+  } else {
+    store_group_vcodes<HD, VB, L>(r.va, r.vb, lane, st);
+  }
+  return store_group_vmeta<HD, L>(r.vm, lane, st);
+}
+
+// fp16 pair (2^-pos of slot 2 m, 2^-pos of slot 2 m + 1): the bit positions of the
+// codes in operand register m (tok_qk)
+template <int KB>
+__device__ __forceinline__ uint32_t tok_posfactors(int m) {
+  if (KB == 2) return (m & 1) ? 0x24002C00u : 0x34003C00u;   // (1/16, 1/64) : (1, 1/4)
+  if (KB == 4) return 0x2C003C00u;                           // (1, 1/16)
+  return kOnes2;
+}
+
+// The q operand of the per-token K products (q' times the position factors) and the
+// group sums Q_g of q' (times 2^-24, the scale of the code products), for this
+// lane's head.
+template <int HD, int KB>
+__device__ __forceinline__ void tok_q_operands(const u4_t (&qb)[HD / 32], u4_t (&qt)[HD / 32],
+                                               float (&qs)[HD / 32]) {
+#pragma unroll
+  for (int g = 0; g < HD / 32; ++g) {
+    float sum = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      qt[g][m] = pkmul(qb[g][m], tok_posfactors<KB>(m));
+      sum = dot2(qb[g][m], kOnes2, sum);
+    }
+    qs[g] = xsum4(sum) * (1.0f / kTwo24);
+  }
+}
+
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(h2_t, w)[0];
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(h2_t, w)[1];
+}
+
+// QK phase of a per-token group: the scores of instances h = 0, 1 times 2^-24 / sl2
+// (the factor kivi_softmax_pv applies for 8-bit K), bias 0.
+template <int HD, int KB, typename L>
+__device__ __forceinline__ QkOut tok_qk(const char* st, const u4_t (&qt)[HD / 32],
+                                        const float (&qs)[HD / 32], int lane, float lazy) {
+  constexpr int NS = HD / 32;
+  constexpr int NW = L::kunits / 4;     // words a lane reads per token
+  const int r = lane & 15;
+  const int g4 = lane >> 4;
+  f4_t out[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const char* kp = st + (16 * h + r) * L::kpitch + g4 * L::kunits;
+    uint32_t w[NW];
+    if constexpr (NW == 1) {
+      w[0] = lds_u32(kp);
+    } else if constexpr (NW == 2) {
+      const u2_t x = lds_u2(kp);
+      w[0] = x[0];
+      w[1] = x[1];
+    } else {
+#pragma unroll
+      for (int k = 0; k < NW / 4; ++k) {
+        const u4_t x = lds_u4(kp + 16 * k);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[4 * k + j] = x[j];
+      }
+    }
+    f4_t dg[NS];
+#pragma unroll
+    for (int g = 0; g < NS; ++g) {
+      u4_t a;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if constexpr (KB == 2) {
+          // operand m: byte m / 2 of the unit; slots 2 m, 2 m + 1 at bit positions
+          // 0, 2 (m even) or 4, 6 (m odd)
+          const uint32_t x = w[g >> 1];
+          a[m] = perm(x, x, sel_bytes(2 * (g & 1) + (m >> 1))) & ((m & 1) ? 0x00C00030u : 0x000C0003u);
+        } else if constexpr (KB == 4) {
+          // operand m: byte m, low nibble (slot 2 m) and high nibble (slot 2 m + 1)
+          a[m] = perm(w[g], w[g], sel_bytes(m)) & 0x00F0000Fu;
+        } else {
+          // operand m: bytes 2 m, 2 m + 1 of the unit
+          const uint32_t x = w[2 * g + (m >> 1)];
+          const uint32_t b0 = 2u * (m & 1);
+          a[m] = perm(x, x, b0 | (0x0cu << 8) | ((b0 + 1u) << 16) | (0x0cu << 24));
+        }
+      }
+      dg[g] = mfma(a, qt[g], f4_t{0.f, 0.f, 0.f, 0.f});
+    }
+    // per-token scale and min of the lane's result rows (tokens 16 h + 4 g4 + e)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const char* mr = st + L::off_kmeta + (16 * h + 4 * g4 + e) * L::kmeta_row;
+      uint32_t sk[2], mk[2];
+      if constexpr (NS == 4) {
+        const u4_t x = lds_u4(mr);
+        sk[0] = x[0]; sk[1] = x[1]; mk[0] = x[2]; mk[1] = x[3];
+      } else {
+        const u2_t x = lds_u2(mr);
+        sk[0] = x[0]; sk[1] = 0u; mk[0] = x[1]; mk[1] = 0u;
+      }
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < NS; ++g) {
+        const uint32_t sw = sk[g >> 1], mw = mk[g >> 1];
+        const float sg = (g & 1) ? half_hi(sw) : half_lo(sw);
+        const float mg = (g & 1) ? half_hi(mw) : half_lo(mw);
+        t = fmaf(sg, dg[g][e], fmaf(mg, qs[g], t));
+      }
+      out[h][e] = t;
+    }
+  }
+  return QkOut{{out[0], out[1]}, 0.f, lazy};
+}
+
+// The wave's per-token groups of the chunk [t_first, t_end): groups wave, wave + 4,
+// ... through the wave's two buffers, the next D groups' loads in flight.
+template <int HD, int KB, int VB>
+__device__ __forceinline__ void tok_wave_groups(const SegDev& s, const SegOffsets& o, int t_first,
+                                                int t_end, int wave, int lane, char* lds,
+                                                u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
+                                                float& sl2) {
+  using L = TokLayout<HD, KB, VB>;
+  using R = TokRegs<HD, KB, VB>;
+  constexpr int D = (KB + VB <= 8) ? 2 : 1;
+  constexpr int NS = HD / 32;
+  const int ng = (t_end - t_first + kTile - 1) / kTile;
+  const int n = (ng - wave + kWaves - 1) / kWaves;
+  if (n <= 0) return;
+  const int t_last = t_end - 1;
+  char* b0 = lds + wave * 2 * L::bytes;
+  char* b1 = b0 + L::bytes;
+  // the ones row of both buffers' V-min block (never overwritten by the groups)
+  if (lane < kTile) {
+    reinterpret_cast<uint16_t*>(b0 + L::off_vm)[NS * L::vms + lane] = 0x3C00;
+    reinterpret_cast<uint16_t*>(b1 + L::off_vm)[NS * L::vms + lane] = 0x3C00;
+  }
+  auto tok = [&](int i) { return t_first + kTile * (wave + kWaves * i); };
+  auto buf = [&](int i) { return (i & 1) ? b1 : b0; };
+  auto load = [&](R& r, int i) { load_tok_group<HD, KB, VB>(r, s, o, tok(i), t_last, lane); };
+  bool big0 = false, big1 = false;
+  auto store = [&](const R& r, int i) {
+    const bool f = store_tok_group<HD, KB, VB>(r, lane, buf(i));
+    if (i & 1) big1 = f;
+    else big0 = f;
+  };
+  R r[D];
+  load(r[0], 0);
+  normalize_q<HD, true>(qb, sl2);
+  u4_t qt[NS];
+  float qs[NS];
+  tok_q_operands<HD, KB>(qb, qt, qs);
+  store(r[0], 0);
+#pragma unroll
+  for (int k = 1; k <= D; ++k)
+    if (k < n) load(r[k % D], k);
+  wave_lds_sync();
+  auto group = [&](int i) {
+    const int nvalid = min(kTile, t_end - tok(i));
+    const QkOut qk = tok_qk<HD, KB, L>(buf(i), qt, qs, lane, ((i & 1) ? big1 : big0) ? 0.f : kLazyLog2);
+    if (nvalid == kTile) kivi_softmax_pv<HD, 8, VB, true, L>(qk, nvalid, buf(i), 0, acc, sl2, lane);
+    else kivi_softmax_pv<HD, 8, VB, false, L>(qk, nvalid, buf(i), 0, acc, sl2, lane);
+  };
+  int i = 0;
+  for (; i + 2 * D < n; i += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      group(i + j);
+      store(r[(j + 1) % D], i + j + 1);
+      load(r[(j + 1) % D], i + j + 1 + D);
+      wave_lds_sync();
+    }
+  }
+  for (; i < n; ++i) {
+    group(i);
+    if (i + 1 < n) {
+      const int set = (i + 1) % D;
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        if (set == k) {
+          store(r[k], i + 1);
+          if (i + 1 + D < n) load(r[k], i + 1 + D);
+        }
+      }
+      wave_lds_sync();
+    }
+  }
+}
+
 // V code position factor of result row e (4 g4 + e of a block): the power of two
 // the PV product of a VB-bit segment carries on that row.
 __device__ __forceinline__ float v_posfactor(int vb, int e) {
@@ -1525,7 +1895,9 @@ __device__ __forceinline__ void touch_params(const DecodeParams& p) {
 
 // Two workgroups (8 waves) per CU: the register budget is capped so a second
 // wave per SIMD hides LDS and dependency latency.
-template <int HD, int MAXB>
+// TOK: the variant for launches of per-token K segments (and FP16 segments); the
+// other variant takes KIVI segments, device tables and FP16 segments.
+template <int HD, int MAXB, bool TOK>
 __global__ void __launch_bounds__(256, 2)
 decode_mfma_kernel(const DecodeParams p) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -1584,14 +1956,39 @@ decode_mfma_kernel(const DecodeParams p) {
   acc.mx = -INFINITY;
   acc.l = 0.f;
 
-  int vb_bits = s.vbits;   // the V width the accumulators carry (KIVI)
-  if (s.kind == kSegTable) {
-    vb_bits = table_entry<HD, MAXB>(s, local, b, kvh, wave, lane, lds, qb, acc, sl2);
-  } else if (s.kind == PK_SEG_FP16) {
+  int vb_bits = s.vbits;   // the V width the accumulators carry (KIVI, per-token K)
+  auto fp16_chunk = [&]() {
     const uint16_t* kbase = reinterpret_cast<const uint16_t*>(s.kd) + b * s.kd_bs + kvh * s.kd_hs;
     const uint16_t* vbase = reinterpret_cast<const uint16_t*>(s.vd) + b * s.vd_bs + kvh * s.vd_hs;
     for (int t0 = t_begin + 32 * wave; t0 < t_end; t0 += 32 * kWaves)
       fp16_group<HD>(kbase, vbase, s.tok_stride, t0, min(32, t_end - t0), qb, acc, sl2, lane);
+  };
+  if constexpr (TOK) {
+    if (s.kind == PK_SEG_FP16) {
+      fp16_chunk();
+    } else if (t_end > t_begin) {
+      SegOffsets o;
+      o.kd = b * s.kd_bs + kvh * s.kd_hs;
+      o.km = b * s.km_bs + kvh * s.km_hs;
+      o.vd = b * s.vd_bs + kvh * s.vd_hs;
+      o.vm = b * s.vm_bs + kvh * s.vm_hs;
+#define PK_TOK_CASE(KB_, VB_)                                                                  \
+  case KB_ * 16 + VB_:                                                                         \
+    if constexpr (KB_ <= MAXB && VB_ <= MAXB)                                                  \
+      tok_wave_groups<HD, KB_, VB_>(s, o, t_begin, t_end, wave, lane, lds, qb, acc, sl2);      \
+    break;
+      switch (s.kbits * 16 + s.vbits) {
+        PK_TOK_CASE(2, 2) PK_TOK_CASE(2, 4) PK_TOK_CASE(2, 8)
+        PK_TOK_CASE(4, 2) PK_TOK_CASE(4, 4) PK_TOK_CASE(4, 8)
+        PK_TOK_CASE(8, 2) PK_TOK_CASE(8, 4) PK_TOK_CASE(8, 8)
+        default: break;
+      }
+#undef PK_TOK_CASE
+    }
+  } else if (s.kind == kSegTable) {
+    vb_bits = table_entry<HD, MAXB>(s, local, b, kvh, wave, lane, lds, qb, acc, sl2);
+  } else if (s.kind == PK_SEG_FP16) {
+    fp16_chunk();
   } else {
     SegOffsets o;
     o.kd = b * s.kd_bs + kvh * s.kd_hs;
@@ -1731,16 +2128,31 @@ inline int kivi_group_bytes_hd(int kb, int vb) {
   return best;
 }
 
-// The launch of one kernel variant (instantiated by one pk_decode_mfma_<HD>_<MAXB>.hip each,
-// so that the variants compile in parallel).
-template <int HD, int MAXB>
+// LDS bytes of one wave's per-token group buffer (widths up to kb / vb bits)
+template <int HD>
+inline int tok_group_bytes_hd(int kb, int vb) {
+  const int sizes[3][3] = {
+      {TokLayout<HD, 2, 2>::bytes, TokLayout<HD, 2, 4>::bytes, TokLayout<HD, 2, 8>::bytes},
+      {TokLayout<HD, 4, 2>::bytes, TokLayout<HD, 4, 4>::bytes, TokLayout<HD, 4, 8>::bytes},
+      {TokLayout<HD, 8, 2>::bytes, TokLayout<HD, 8, 4>::bytes, TokLayout<HD, 8, 8>::bytes}};
+  int best = 0;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j)
+      if ((2 << i) <= kb && (2 << j) <= vb) best = std::max(best, sizes[i][j]);
+  return best;
+}
+
+// The launch of one kernel variant (instantiated by one pk_decode_mfma[_tok]_<HD>_<MAXB>.hip
+// each, so that the variants compile in parallel).
+template <int HD, int MAXB, bool TOK>
 int launch_decode_mfma_variant(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_mfma_kernel<HD, MAXB>), grid, dim3(256), lds, stream, dp);
+  hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_mfma_kernel<HD, MAXB, TOK>), grid, dim3(256), lds, stream, dp);
   return check_launch("decode_mfma");
 }
 
-#define PK_DECLARE_MFMA_VARIANT(HD_, MB_) \
-  int launch_decode_mfma_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream);
+#define PK_DECLARE_MFMA_VARIANT(HD_, MB_)                                                        \
+  int launch_decode_mfma_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream); \
+  int launch_decode_mfma_tok_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream);
 PK_DECLARE_MFMA_VARIANT(64, 2)
 PK_DECLARE_MFMA_VARIANT(64, 4)
 PK_DECLARE_MFMA_VARIANT(64, 8)
@@ -1752,14 +2164,21 @@ PK_DECLARE_MFMA_VARIANT(128, 8)
 }  // namespace pk
 
 #ifdef PK_MFMA_HD
-// one variant of the kernel per translation unit
+// one variant of the kernel per translation unit (PK_MFMA_TOK: the per-token K variant)
 namespace pk {
 #define PK_CAT3(a, b, c) a##b##_##c
+#ifdef PK_MFMA_TOK
+#define PK_VARIANT_NAME(HD_, MB_) PK_CAT3(launch_decode_mfma_tok_, HD_, MB_)
+#define PK_VARIANT_TOK true
+#else
 #define PK_VARIANT_NAME(HD_, MB_) PK_CAT3(launch_decode_mfma_, HD_, MB_)
+#define PK_VARIANT_TOK false
+#endif
 int PK_VARIANT_NAME(PK_MFMA_HD, PK_MFMA_MAXB)(const DecodeParams& dp, dim3 grid, size_t lds,
                                               hipStream_t stream) {
-  return launch_decode_mfma_variant<PK_MFMA_HD, PK_MFMA_MAXB>(dp, grid, lds, stream);
+  return launch_decode_mfma_variant<PK_MFMA_HD, PK_MFMA_MAXB, PK_VARIANT_TOK>(dp, grid, lds, stream);
 }
+#undef PK_VARIANT_TOK
 #undef PK_VARIANT_NAME
 #undef PK_CAT3
 }  // namespace pk

@@ -245,7 +245,8 @@ class Problem:
     C structure, with its keep-alive list."""
 
     def __init__(self, q: torch.Tensor, segments: List[Segment], num_attention_heads: int,
-                 generic_kernel: bool = False, table: Optional[SegmentTable] = None):
+                 generic_kernel: bool = False, table: Optional[SegmentTable] = None,
+                 require_mfma: bool = False):
         if not segments and (table is None or table.count == 0):
             raise ValueError("no KV to attend: every tier is empty")
         if q.dim() == 2:
@@ -284,7 +285,10 @@ class Problem:
         p.q_bstride, p.q_hstride = q.stride(0), q.stride(1)
         p.segments = ctypes.cast(arr, ctypes.POINTER(_lib.PkSegment))
         p.num_segments = len(segments)
-        p.flags = _lib.PK_FLAG_GENERIC_KERNEL if generic_kernel else 0
+        if generic_kernel and require_mfma:
+            raise ValueError("generic_kernel and require_mfma exclude each other")
+        p.flags = (_lib.PK_FLAG_GENERIC_KERNEL if generic_kernel else 0) | \
+            (_lib.PK_FLAG_REQUIRE_MFMA if require_mfma else 0)
         if table is not None and table.count:
             p.table = table.buf.data_ptr()
             p.table_count = table.count
