@@ -194,6 +194,86 @@ def _bench_long_generation(device, steps, warmup, stream, generated=1056):
     return res
 
 
+# The reference's published legacy numbers (RTX 4080 SUPER, split-K kernel at its best
+# split count, ms; results/kernel_decode_bench.md:9-16), keyed by (S, bits).
+LEGACY_PUBLISHED_MS = {(4096, 2): 0.1321, (4096, 4): 0.24576, (8192, 2): 0.22323,
+                       (8192, 4): 0.29082, (16384, 2): 0.40346, (16384, 4): 0.54374,
+                       (32768, 2): 0.76595, (32768, 4): 1.05165}
+
+
+def _bench_legacy(device, S, bits, steps, warmup, stream, with_dense=True, with_grid=True):
+    """The reference's legacy per-token layout at its published shape (Hq 28, Hkv 4, hd 128,
+    group 32, prompt only, K and V packed per token at ``bits``; seeded N(0,1) K/V/q as
+    scripts/bench_decode_kernel.py:66-84): the planner's launch, the reference's split grid
+    (8 .. 128 splits, best), the partials kernel alone, and the GQA-aware FP16 kernel over the
+    same tokens."""
+    from phasekv_amd import decode as dec
+    from phasekv_amd.kernels import attention_triton as at
+    from phasekv_amd.kernels.packing import quantize_pack
+    hq, hkv, hd = 28, 4, 128
+    g = torch.Generator().manual_seed(1234)
+    K = torch.randn(hkv, S, hd, generator=g).to(torch.float16).to(device)
+    V = torch.randn(hkv, S, hd, generator=g).to(torch.float16).to(device)
+    q = torch.randn(hq, hd, generator=g).to(torch.float16).to(device)
+    pk = quantize_pack(K, bits, -1, 32)
+    pv = quantize_pack(V, bits, -1, 32)
+    kv_bytes = sum(t.numel() * t.element_size() for pt in (pk, pv)
+                   for t in (pt.packed, pt.scale, pt.mins))
+    nbytes = kv_bytes + 2 * 2 * hq * hd
+    copies = _copies_for(nbytes)
+    clone = lambda pt: type(pt)(pt.packed.clone(), pt.scale.clone(), pt.mins.clone(), pt.bits,
+                                pt.axis, pt.group_size, pt.orig_shape, pt.axis_len)
+    sets = [(pk, pv)] + [(clone(pk), clone(pv)) for _ in range(copies - 1)]
+    probs = [dec.Problem(q, [dec.packed_segment(a, b, batched=False)], hq, require_mfma=True)
+             for a, b in sets]
+    sec = _time_graph([lambda pr=pr: dec.fused_decode(pr) for pr in probs], steps, warmup, stream)
+    ksec = _time_graph([lambda pr=pr: dec.launch_partials(pr) for pr in probs], steps, warmup,
+                       stream)
+    grid = {}
+    for ns in ((8, 16, 32, 64, 128) if with_grid else ()):
+        grid[ns] = _time_graph([lambda a=a, b=b: at.decode_attention_packed_splitk(
+            q, a, b, hq, num_splits=ns) for a, b in sets], steps, warmup, stream)
+    best_ns = min(grid, key=grid.get) if grid else None
+    ref_ms = LEGACY_PUBLISHED_MS.get((S, bits))
+    res = {"config": f"legacy-S{S}-{bits}b", "shape": "Hq28/Hkv4/hd128, per-token K and V",
+           "S": S, "bits": bits, "bytes": nbytes, "copies": copies,
+           "timed_distinct_bytes": min(steps, copies) * nbytes,
+           "us_per_step": sec * 1e6, "gbs": nbytes / sec / 1e9,
+           "partials_us": ksec * 1e6, "partials_gbs": nbytes / ksec / 1e9,
+           "splitk_grid_us": {str(k): round(v * 1e6, 3) for k, v in grid.items()},
+           "splitk_best_us": grid[best_ns] * 1e6 if grid else None, "splitk_best_splits": best_ns,
+           "ref_published_splitk_us": ref_ms * 1e3 if ref_ms else None}
+    res["frac"] = res["gbs"] / HBM_PEAK_GBS
+    res["partials_frac"] = res["partials_gbs"] / HBM_PEAK_GBS
+    if ref_ms:
+        res["speedup_vs_ref_published"] = ref_ms * 1e-3 / sec
+    del sets, probs
+    if with_dense:
+        dbytes = 2 * hkv * S * hd * 2 + 2 * 2 * hq * hd
+        dcopies = _copies_for(dbytes, 64)
+        dsets = [(K, V)] + [(K.clone(), V.clone()) for _ in range(dcopies - 1)]
+        dprobs = [dec.Problem(q, [dec.fp16_segment(k, v, batched=False)], hq) for k, v in dsets]
+        dsec = _time_graph([lambda pr=pr: dec.fused_decode(pr) for pr in dprobs], steps, warmup,
+                           stream)
+        res["fp16_dense_us"] = dsec * 1e6
+        res["fp16_dense_gbs"] = dbytes / dsec / 1e9
+        res["speedup_vs_fp16"] = dsec / sec
+        del dsets, dprobs
+    torch.cuda.empty_cache()
+    return res
+
+
+def _legacy_rows(device, steps, warmup, stream, with_dense=True, with_grid=True,
+                 lengths=(4096, 8192, 16384, 32768), widths=(2, 4)):
+    rows = []
+    for S in lengths:
+        for bits in widths:
+            r = _bench_legacy(device, S, bits, steps, warmup, stream, with_dense, with_grid)
+            _log(f"bench: legacy {r}")
+            rows.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+    return rows
+
+
 def _bench_prefill_pack(device, steps, warmup, stream):
     """C4's prefill side: an 8192 x 4 x 128 fp16 K/V block packed to the 2-bit prompt tier.
 
@@ -496,6 +576,13 @@ def main() -> int:
                     help="time only the prefill side (C4 pack, prompt selection) and print its line")
     ap.add_argument("--long-generation", action="store_true",
                     help="time only the C2 cache after 1056 generated tokens (64 cold segments)")
+    ap.add_argument("--legacy", action="store_true",
+                    help="time only the legacy per-token layout at the reference's published "
+                         "shape and print its line")
+    ap.add_argument("--legacy-lengths", type=int, nargs="+", default=[4096, 8192, 16384, 32768])
+    ap.add_argument("--legacy-bits", type=int, nargs="+", default=[2, 4])
+    ap.add_argument("--no-grid", action="store_true",
+                    help="legacy rows without the reference's split-count grid")
     ap.add_argument("--lifecycle", action="store_true",
                     help="time only the hot window lifecycle (append, cooling) and print its line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -542,6 +629,16 @@ def main() -> int:
                           "n_gpus": 1, "config": {"workload": r["config"]}, "rows": [r]}),
               flush=True)
         return 0
+    if args.legacy:
+        rows = _legacy_rows(device, min(args.steps, 256), min(args.warmup, 256), stream,
+                            not args.no_dense, not args.no_grid, args.legacy_lengths,
+                            args.legacy_bits)
+        print(json.dumps({"metric": "legacy per-token layout decode-attn µs/step, Hq28/Hkv4/"
+                                    "hd128, prompt only, S 4K-32K, 2/4-bit",
+                          "value": rows[-1]["us_per_step"], "unit": "µs",
+                          "higher_is_better": False, "n_gpus": 1,
+                          "config": {"workload": rows[-1]["config"]}, "rows": rows}), flush=True)
+        return 0
     if args.lifecycle:
         rows = []
         for name, ratio in (("C2", 1.0), ("C2", 0.5), ("C5", 0.5)):
@@ -571,6 +668,8 @@ def main() -> int:
                 r["cpu_baseline"] = _cpu_baseline("C1", min(args.cpu_seconds, 5.0))
             _log(f"bench: {name} {r}")
             sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+        sweep.extend(_legacy_rows(device, min(args.steps, 256), min(args.warmup, 256), stream,
+                                  not args.no_dense))
         r = _bench_long_generation(device, min(args.steps, 256), min(args.warmup, 256), stream)
         _log(f"bench: long generation {r}")
         sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
