@@ -600,6 +600,8 @@ def main() -> int:
     device = torch.device("cuda:0")
     stream = torch.cuda.Stream(device)
     cfg = workloads.CONFIGS[args.config]
+    if args.copy_probe_mib > 0:
+        _copy_probe(args.copy_probe_mib, device)
     if args.e2e:
         rows = [_bench_e2e(device, L, 4, 32) for L in (4096, 16384, 32768)]
         rows = [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
@@ -651,8 +653,6 @@ def main() -> int:
                           "config": {"workload": "C2 cache shape, keep all"}, "rows": rows}),
               flush=True)
         return 0
-    if args.copy_probe_mib > 0:
-        _copy_probe(args.copy_probe_mib, device)
     _log(f"bench: {cfg} steps={args.steps} warmup={args.warmup}")
     main_res, _ = _bench_config(cfg, device, args.steps, args.warmup, stream,
                                 with_dense=not args.no_dense)
