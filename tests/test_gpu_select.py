@@ -83,3 +83,21 @@ def test_errors(gpu):
     with pytest.raises(ValueError, match="key length"):
         select_prompt_indices([a], prompt_len=15, model_config=_Cfg(2), prefill_keep_ratio=0.5,
                               sink_tokens=1, obs_window=2, pool_kernel=3, pooling="maxpool")
+
+
+@pytest.mark.parametrize("pooling,kernel", [("maxpool", 7), ("avgpool", 5)])
+@pytest.mark.parametrize("L", [20000, 32768])
+def test_long_prompts_beyond_the_lds_staging(gpu, pooling, kernel, L):
+    """Rows of more than 18432 candidates: the kernel recomputes the pooled keys from the
+    global votes on every radix and scan pass instead of staging them in LDS."""
+    from phasekv_amd.prompt_tier import select_prompt_indices
+    print(f"case L={L} {pooling} {kernel}", flush=True)
+    B, hkv, g, obs = 1, 2, 4, 32
+    attns = [_attn(L + 7, B, hkv * g, obs, L)]
+    kw = dict(prompt_len=L, prefill_keep_ratio=0.1, sink_tokens=4, obs_window=obs,
+              pool_kernel=kernel, pooling=pooling)
+    got = select_prompt_indices([a.to(gpu) for a in attns], model_config=_Cfg(hkv), **kw)
+    want = so.select_prompt_indices([a.numpy() for a in attns], num_kv_heads=hkv, **kw)
+    for gl, wl in zip(got, want):
+        assert gl.dtype == torch.int64 and tuple(gl.shape) == wl.shape
+        assert np.array_equal(gl.cpu().numpy(), wl)
