@@ -92,8 +92,10 @@ struct DecodeParams {
   SegDev seg[kMaxSeg];
 };
 
-// MFMA fast path (pk_decode_mfma.hip): same parameters and partial layout.
+// MFMA fast path (pk_decode_mfma.hip): same parameters and partial layout.  waves: 4, or 8
+// for a launch whose segments all take the wave-private group path (no device table,
+// codes up to 4 bits).
 int launch_decode_mfma(const DecodeParams& dp, int lchunks, int max_kbits, int max_vbits,
-                       hipStream_t stream);
+                       int waves, hipStream_t stream);
 
 }  // namespace pk

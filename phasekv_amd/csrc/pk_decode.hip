@@ -426,6 +426,13 @@ static int64_t env_int(const char* name, int64_t dflt) {
   return std::max<int64_t>(1, atoll(v));
 }
 
+static double env_double(const char* name, double dflt) {
+  const char* v = getenv(name);
+  if (!v || !*v) return dflt;
+  const double x = atof(v);
+  return x > 0 ? x : dflt;
+}
+
 // Relative cost of a 32-token group in the MFMA kernel (measured on MI355X at
 // batch 8, hd 128): 2/2-bit 100, 4/4-bit 118, 2/8-bit 150, 8/8-bit 190, fp16 280.
 static int group_weight(const pk_segment& s) {
@@ -436,15 +443,26 @@ static int group_weight(const pk_segment& s) {
   return lo == 2 ? 150 : lo == 4 ? 165 : 190;
 }
 
+static bool wave_path_only(const pk_decode_problem* p);
+
+// Per-group factor of a chunk on an eight-wave workgroup (a wave's group chain shared
+// with the SIMD's second wave), fitted on the legacy 16K / 32K rows: -0.5 µs per step.
+constexpr double kPlanWave8Factor = 1.6;
+
 // Automatic plan of the MFMA kernel: per-segment chunk lengths (whole 32-token
 // groups, at least one per wave) sized by group weight, so every chunk costs about the same whatever its segment's bit
 // widths, and the number of chunks per row chosen among a few candidates around
 // one and two workgroups per CU by an estimate of the finishing time (fitted to
 // MI355X measurements): chunk cost = 5 + groups per wave * weight * t, t = 1
 // alone on a CU and 1.8 with a second workgroup; workgroups beyond two per CU run
-// as the cheapest chunks (launch order), so they add about half a cheap chunk.
+// as the cheapest chunks (launch order), so they add about half a cheap chunk.  A plan
+// of at most one workgroup per CU with chunks of 8 or more groups runs eight waves per
+// workgroup where the segments allow it (launch_partials): groups per wave halve, at
+// factor kPlanWave8Factor.
+
 static void plan_weighted(const pk_decode_problem* p, int64_t per_bh, Plan& pl) {
   const int ns = p->num_segments;
+  const bool wave8 = wave_path_only(p);
   std::vector<int64_t> G(ns), w(ns);
   int64_t row = 0;
   for (int i = 0; i < ns; ++i) {
@@ -463,7 +481,14 @@ static void plan_weighted(const pk_decode_problem* p, int64_t per_bh, Plan& pl) 
       wgs += cdiv(G[i], g[i]) * per_bh;
     }
     const double t = wgs <= cus ? 1.0 : 1.8;
+    // eight waves per workgroup (launch_partials) when the launch fits one workgroup per CU
+    // and its chunks hold 8 or more groups: the groups spread over twice the waves
+    int64_t gmin = INT64_MAX;
+    for (int i = 0; i < ns; ++i) gmin = std::min(gmin, g[i]);
+    const double w8t = env_double("PK_PLAN_W8T", kPlanWave8Factor);
+    const bool w8 = w8t > 0 && wave8 && wgs <= cus && gmin >= 8;
     auto cost = [&](int64_t groups, int64_t wi) {
+      if (w8) return 5.0 + std::ceil(groups / 8.0) * (double)wi / 100.0 * w8t;
       return 5.0 + std::ceil(groups / 4.0) * (double)wi / 100.0 * t;
     };
     double cmax = 0, cmin = 1e30, total = 0;
@@ -651,6 +676,27 @@ static size_t generic_lds_bytes(const Plan& pl, int hd) {
                           (size_t)pl.HS * pl.tile + 3 * pl.HS);
 }
 
+// Whether every segment of the problem takes the MFMA kernel's wave-private group path
+// (what the 8-wave variants compile): FP16 segments, per-token K segments and KIVI segments
+// in quantize_pack's storage (token-major codes, group-major metadata 8-byte aligned), codes
+// up to 4 bits, no device table.
+static bool wave_path_only(const pk_decode_problem* p) {
+  if (p->table_count > 0) return false;
+  for (int i = 0; i < p->num_segments; ++i) {
+    const pk_segment& s = p->segments[i];
+    if (s.kind == PK_SEG_FP16) continue;
+    if (s.k_bits > 4 || s.v_bits > 4) return false;
+    if (s.kind == PK_SEG_TOKEN) continue;
+    if (s.k_data_layout != PK_CODES_TOKEN_MAJOR || s.k_meta_layout != PK_META_GROUP_MAJOR)
+      return false;
+    if (!aligned(s.k_scale, 8) || !aligned(s.k_mins, 8) || s.k_meta_bstride % 4 ||
+        s.k_meta_hstride % 4)
+      return false;
+    if (cdiv((int64_t)s.length * s.k_bits, 8) >= ((int64_t)1 << 31) / p->head_dim) return false;
+  }
+  return true;
+}
+
 static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
                            hipStream_t stream) {
   DecodeParams dp{};
@@ -702,7 +748,18 @@ static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
     dp.order = pl.order;
     int rc;
     if (pl.mfma) {
-      rc = launch_decode_mfma(dp, lchunks, pl.max_kbits, pl.max_vbits, stream);
+      // a launch of at most one workgroup per CU whose chunks hold 8 or more groups runs
+      // eight waves per workgroup where every segment allows it: two waves per SIMD hide
+      // each other's group chains (measured: C3-32K -1.1 µs; with fewer groups per chunk
+      // the idle waves and the wider merge cost more, C2 +0.4 µs)
+      const int64_t wgs = (int64_t)lchunks * p->num_kv_heads * pl.nslab * p->batch;
+      int max_groups = 0;
+      for (int i = 0; i < n; ++i)
+        if (dp.seg[i].kind != kSegTable) max_groups = std::max(max_groups, (dp.seg[i].chunk_len + 31) / 32);
+      const char* w8 = getenv("PK_WAVES8");   // "0": four waves always, for experiments
+      const int waves = (wgs <= device_cu_count() && max_groups >= 8 && wave_path_only(p) &&
+                         !(w8 && w8[0] == '0')) ? 8 : 4;
+      rc = launch_decode_mfma(dp, lchunks, pl.max_kbits, pl.max_vbits, waves, stream);
     } else {
       dim3 grid(lchunks, p->num_kv_heads * pl.nslab, p->batch);
       hipLaunchKernelGGL(decode_partials_generic, grid, dim3(kThreads), lds, stream, dp);

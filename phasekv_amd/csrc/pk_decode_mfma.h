@@ -1424,8 +1424,10 @@ __device__ __forceinline__ void kivi_wave_groups(const SegDev& s, const SegOffse
   }
 }
 
-// Stages of the chunk: t_first + i t_stride (i < nst), tokens below t_end.
-template <int HD, int KB, int VB, int MAXB>
+// Stages of the chunk: t_first + i t_stride (i < nst), tokens below t_end.  NW: waves of
+// the workgroup.  The 8-wave variants take only what the wave-private groups read (the host
+// checks it); the 128-token workgroup stages need 4 waves.
+template <int HD, int KB, int VB, int MAXB, int NW>
 __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_first,
                                            int t_stride, int nst, int t_end, int wave, int lane,
                                            int tid, char* lds, int stage_bytes,
@@ -1450,18 +1452,20 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
   kl.kmeta4 = !s.kmeta_gm && (kl.row_groups % 4 == 0) && (t_first % kStage == 0) &&
               (t_stride % kStage == 0) && meta8;
   if constexpr (KB <= 4 && VB <= 4) {
-    if (kl.kdata_tm && kl.kmeta_gm && kl.row_bytes < ((int64_t)1 << 31) / HD) {
-      kivi_wave_groups<HD, KB, VB>(s, o, kl, t_first, t_end, wave, wave, kWaves, lane, lds,
+    if (NW != kWaves || (kl.kdata_tm && kl.kmeta_gm && kl.row_bytes < ((int64_t)1 << 31) / HD)) {
+      kivi_wave_groups<HD, KB, VB>(s, o, kl, t_first, t_end, wave, wave, NW, lane, lds,
                                    2 * GroupLayout<HD, KB, VB>::bytes, qb, acc, sl2, true);
       return;
     }
   }
-  if (kl.kmode == 16 && (kl.kmeta4 || kl.kmeta_gm) && kl.row_bytes < ((int64_t)1 << 31) / HD)
-    kivi_stages<HD, KB, VB, MAXB, true>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
-                                  stage_bytes, qb, acc, sl2);
-  else
-    kivi_stages<HD, KB, VB, MAXB, false>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
-                                   stage_bytes, qb, acc, sl2);
+  if constexpr (NW == kWaves) {
+    if (kl.kmode == 16 && (kl.kmeta4 || kl.kmeta_gm) && kl.row_bytes < ((int64_t)1 << 31) / HD)
+      kivi_stages<HD, KB, VB, MAXB, true>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
+                                    stage_bytes, qb, acc, sl2);
+    else
+      kivi_stages<HD, KB, VB, MAXB, false>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
+                                     stage_bytes, qb, acc, sl2);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1728,7 +1732,7 @@ __device__ __forceinline__ QkOut tok_qk(const char* st, const u4_t (&qt)[HD / 32
 
 // The wave's per-token groups of the chunk [t_first, t_end): groups wave, wave + 4,
 // ... through the wave's two buffers, the next D groups' loads in flight.
-template <int HD, int KB, int VB>
+template <int HD, int KB, int VB, int NW>
 __device__ __forceinline__ void tok_wave_groups(const SegDev& s, const SegOffsets& o, int t_first,
                                                 int t_end, int wave, int lane, char* lds,
                                                 u4_t (&qb)[HD / 32], WaveAcc<HD>& acc,
@@ -1738,7 +1742,7 @@ __device__ __forceinline__ void tok_wave_groups(const SegDev& s, const SegOffset
   constexpr int D = (KB + VB <= 8) ? 2 : 1;
   constexpr int NS = HD / 32;
   const int ng = (t_end - t_first + kTile - 1) / kTile;
-  const int n = (ng - wave + kWaves - 1) / kWaves;
+  const int n = (ng - wave + NW - 1) / NW;
   if (n <= 0) return;
   const int t_last = t_end - 1;
   char* b0 = lds + wave * 2 * L::bytes;
@@ -1748,7 +1752,7 @@ __device__ __forceinline__ void tok_wave_groups(const SegDev& s, const SegOffset
     reinterpret_cast<uint16_t*>(b0 + L::off_vm)[NS * L::vms + lane] = 0x3C00;
     reinterpret_cast<uint16_t*>(b1 + L::off_vm)[NS * L::vms + lane] = 0x3C00;
   }
-  auto tok = [&](int i) { return t_first + kTile * (wave + kWaves * i); };
+  auto tok = [&](int i) { return t_first + kTile * (wave + NW * i); };
   auto buf = [&](int i) { return (i & 1) ? b1 : b0; };
   auto load = [&](R& r, int i) { load_tok_group<HD, KB, VB>(r, s, o, tok(i), t_last, lane); };
   bool big0 = false, big1 = false;
@@ -1896,9 +1900,12 @@ __device__ __forceinline__ void touch_params(const DecodeParams& p) {
 // Two workgroups (8 waves) per CU: the register budget is capped so a second
 // wave per SIMD hides LDS and dependency latency.
 // TOK: the variant for launches of per-token K segments (and FP16 segments); the
-// other variant takes KIVI segments, device tables and FP16 segments.
-template <int HD, int MAXB, bool TOK>
-__global__ void __launch_bounds__(256, 2)
+// other variant takes KIVI segments, device tables and FP16 segments.  NW: waves per
+// workgroup, 4 (two workgroups per CU) or 8 (one workgroup of two waves per SIMD, for
+// launches of at most one workgroup per CU whose segments all take the wave-private
+// group path; no device tables).
+template <int HD, int MAXB, bool TOK, int NW>
+__global__ void __launch_bounds__(64 * NW, 8 / NW)
 decode_mfma_kernel(const DecodeParams p) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr int NB = HD / 16;
@@ -1960,7 +1967,7 @@ decode_mfma_kernel(const DecodeParams p) {
   auto fp16_chunk = [&]() {
     const uint16_t* kbase = reinterpret_cast<const uint16_t*>(s.kd) + b * s.kd_bs + kvh * s.kd_hs;
     const uint16_t* vbase = reinterpret_cast<const uint16_t*>(s.vd) + b * s.vd_bs + kvh * s.vd_hs;
-    for (int t0 = t_begin + 32 * wave; t0 < t_end; t0 += 32 * kWaves)
+    for (int t0 = t_begin + 32 * wave; t0 < t_end; t0 += 32 * NW)
       fp16_group<HD>(kbase, vbase, s.tok_stride, t0, min(32, t_end - t0), qb, acc, sl2, lane);
   };
   if constexpr (TOK) {
@@ -1975,7 +1982,7 @@ decode_mfma_kernel(const DecodeParams p) {
 #define PK_TOK_CASE(KB_, VB_)                                                                  \
   case KB_ * 16 + VB_:                                                                         \
     if constexpr (KB_ <= MAXB && VB_ <= MAXB)                                                  \
-      tok_wave_groups<HD, KB_, VB_>(s, o, t_begin, t_end, wave, lane, lds, qb, acc, sl2);      \
+      tok_wave_groups<HD, KB_, VB_, NW>(s, o, t_begin, t_end, wave, lane, lds, qb, acc, sl2);  \
     break;
       switch (s.kbits * 16 + s.vbits) {
         PK_TOK_CASE(2, 2) PK_TOK_CASE(2, 4) PK_TOK_CASE(2, 8)
@@ -1986,7 +1993,8 @@ decode_mfma_kernel(const DecodeParams p) {
 #undef PK_TOK_CASE
     }
   } else if (s.kind == kSegTable) {
-    vb_bits = table_entry<HD, MAXB>(s, local, b, kvh, wave, lane, lds, qb, acc, sl2);
+    if constexpr (NW == kWaves)
+      vb_bits = table_entry<HD, MAXB>(s, local, b, kvh, wave, lane, lds, qb, acc, sl2);
   } else if (s.kind == PK_SEG_FP16) {
     fp16_chunk();
   } else {
@@ -2005,7 +2013,7 @@ decode_mfma_kernel(const DecodeParams p) {
 #define PK_KIVI_CASE(KB_, VB_)                                                                 \
   case KB_ * 16 + VB_:                                                                         \
     if constexpr (KB_ <= MAXB && VB_ <= MAXB)                                                  \
-      kivi_chunk<HD, KB_, VB_, MAXB>(s, o, kt_first, kt_stride, knst, kt_end, wave, lane, tid, lds,  \
+      kivi_chunk<HD, KB_, VB_, MAXB, NW>(s, o, kt_first, kt_stride, knst, kt_end, wave, lane, tid, lds,  \
                                      p.stage_lds, qb, acc, sl2);                               \
     break;
     if (knst > 0) {
@@ -2033,9 +2041,9 @@ decode_mfma_kernel(const DecodeParams p) {
   // rows padded by 16 bytes: the 16 rows of one 16-byte store start 4 banks apart
   // (unpadded, every row of a store would hit the same 4 banks)
   constexpr int MP = HD + 4;
-  float* mo = reinterpret_cast<float*>(lds);               // [4][16][MP]
-  float* mm = mo + kWaves * 16 * MP;                        // [4][16]
-  float* ml = mm + kWaves * 16;                             // [4][16]
+  float* mo = reinterpret_cast<float*>(lds);               // [NW][16][MP]
+  float* mm = mo + NW * 16 * MP;                            // [NW][16]
+  float* ml = mm + NW * 16;                                 // [NW][16]
   float l_full;
   if (s.kind == PK_SEG_FP16) {
     l_full = xsum4(acc.l);
@@ -2071,12 +2079,12 @@ decode_mfma_kernel(const DecodeParams p) {
   // thread -> (head, 4 channels): the four waves' weights once per head, then
   // one 16-byte read per wave and one 16-byte store
   constexpr int Q = HD / 4;
-  for (int i = tid; i < nh * Q; i += 256) {
+  for (int i = tid; i < nh * Q; i += 64 * NW) {
     const int hh = i / Q, c = 4 * (i - hh * Q);
-    float mw[kWaves];
+    float mw[NW];
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       mw[w] = mm[w * 16 + hh];
       M = fmaxf(M, mw[w]);
     }
@@ -2084,7 +2092,7 @@ decode_mfma_kernel(const DecodeParams p) {
     float L = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < NW; ++w) {
         const float wt = __builtin_amdgcn_exp2f(mw[w] - M);
         o += wt * *reinterpret_cast<const f4_t*>(mo + (w * 16 + hh) * MP + c);
         L += wt * ml[w * 16 + hh];
@@ -2144,39 +2152,59 @@ inline int tok_group_bytes_hd(int kb, int vb) {
 
 // The launch of one kernel variant (instantiated by one pk_decode_mfma[_tok]_<HD>_<MAXB>.hip
 // each, so that the variants compile in parallel).
-template <int HD, int MAXB, bool TOK>
+template <int HD, int MAXB, bool TOK, int NW>
 int launch_decode_mfma_variant(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_mfma_kernel<HD, MAXB, TOK>), grid, dim3(256), lds, stream, dp);
+  hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_mfma_kernel<HD, MAXB, TOK, NW>), grid, dim3(64 * NW), lds,
+                     stream, dp);
   return check_launch("decode_mfma");
 }
 
 #define PK_DECLARE_MFMA_VARIANT(HD_, MB_)                                                        \
   int launch_decode_mfma_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream); \
   int launch_decode_mfma_tok_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream);
+#define PK_DECLARE_MFMA_W8_VARIANT(HD_, MB_)                                                     \
+  int launch_decode_mfma_w8_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream); \
+  int launch_decode_mfma_tok_w8_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream);
 PK_DECLARE_MFMA_VARIANT(64, 2)
 PK_DECLARE_MFMA_VARIANT(64, 4)
 PK_DECLARE_MFMA_VARIANT(64, 8)
 PK_DECLARE_MFMA_VARIANT(128, 2)
 PK_DECLARE_MFMA_VARIANT(128, 4)
 PK_DECLARE_MFMA_VARIANT(128, 8)
+PK_DECLARE_MFMA_W8_VARIANT(64, 2)
+PK_DECLARE_MFMA_W8_VARIANT(64, 4)
+PK_DECLARE_MFMA_W8_VARIANT(128, 2)
+PK_DECLARE_MFMA_W8_VARIANT(128, 4)
+#undef PK_DECLARE_MFMA_W8_VARIANT
 #undef PK_DECLARE_MFMA_VARIANT
 
 }  // namespace pk
 
 #ifdef PK_MFMA_HD
-// one variant of the kernel per translation unit (PK_MFMA_TOK: the per-token K variant)
+// one variant of the kernel per translation unit (PK_MFMA_TOK: the per-token K variant;
+// PK_MFMA_W8: eight waves per workgroup)
+#ifndef PK_MFMA_W8
+#define PK_MFMA_W8 0
+#endif
 namespace pk {
 #define PK_CAT3(a, b, c) a##b##_##c
-#ifdef PK_MFMA_TOK
+#if defined(PK_MFMA_TOK) && PK_MFMA_W8
+#define PK_VARIANT_NAME(HD_, MB_) PK_CAT3(launch_decode_mfma_tok_w8_, HD_, MB_)
+#define PK_VARIANT_TOK true
+#elif defined(PK_MFMA_TOK)
 #define PK_VARIANT_NAME(HD_, MB_) PK_CAT3(launch_decode_mfma_tok_, HD_, MB_)
 #define PK_VARIANT_TOK true
+#elif PK_MFMA_W8
+#define PK_VARIANT_NAME(HD_, MB_) PK_CAT3(launch_decode_mfma_w8_, HD_, MB_)
+#define PK_VARIANT_TOK false
 #else
 #define PK_VARIANT_NAME(HD_, MB_) PK_CAT3(launch_decode_mfma_, HD_, MB_)
 #define PK_VARIANT_TOK false
 #endif
 int PK_VARIANT_NAME(PK_MFMA_HD, PK_MFMA_MAXB)(const DecodeParams& dp, dim3 grid, size_t lds,
                                               hipStream_t stream) {
-  return launch_decode_mfma_variant<PK_MFMA_HD, PK_MFMA_MAXB, PK_VARIANT_TOK>(dp, grid, lds, stream);
+  return launch_decode_mfma_variant<PK_MFMA_HD, PK_MFMA_MAXB, PK_VARIANT_TOK,
+                                    PK_MFMA_W8 ? 8 : kWaves>(dp, grid, lds, stream);
 }
 #undef PK_VARIANT_TOK
 #undef PK_VARIANT_NAME

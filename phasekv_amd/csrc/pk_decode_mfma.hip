@@ -20,26 +20,43 @@ static int tok_group_bytes(int hd, int kb, int vb) {
 }
 
 int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, int max_vbits,
-                       hipStream_t stream) {
+                       int waves, hipStream_t stream) {
   DecodeParams dp = dp_in;
   const int hd = dp.hd;
   // per-token K segments go to the TOK variant (the host never mixes them with KIVI
   // segments or a device table in one launch)
   bool tok = false;
   for (int i = 0; i < dp.nseg; ++i) tok = tok || dp.seg[i].kind == PK_SEG_TOKEN;
+  const int maxb = std::max(max_kbits, max_vbits);
+  const bool w8 = waves == 8 && maxb <= 4;
+  const size_t nw = w8 ? 8 : kWaves;
   size_t staging;
   if (tok) {
     dp.stage_lds = 0;
-    staging = (size_t)kWaves * 2 * tok_group_bytes(hd, max_kbits, max_vbits);
+    staging = nw * 2 * tok_group_bytes(hd, max_kbits, max_vbits);
+  } else if (w8) {
+    dp.stage_lds = 0;
+    staging = nw * 2 * kivi_group_bytes(hd, max_kbits, max_vbits);
   } else {
     dp.stage_lds = (kivi_stage_bytes(hd, max_kbits, max_vbits) + 15) & ~15;
     staging = std::max(2 * (size_t)dp.stage_lds,
                        (size_t)kWaves * 2 * kivi_group_bytes(hd, max_kbits, max_vbits));
   }
-  const size_t merge = sizeof(float) * ((size_t)kWaves * 16 * (hd + 4) + 2 * kWaves * 16);
+  const size_t merge = sizeof(float) * (nw * 16 * (hd + 4) + 2 * nw * 16);
   const size_t lds = std::max(staging, merge);
   const dim3 grid(lchunks, dp.Hkv * dp.nslab, dp.B);
-  const int maxb = std::max(max_kbits, max_vbits);
+  if (w8) {
+    if (tok) {
+      if (hd == 128) return maxb <= 2 ? launch_decode_mfma_tok_w8_128_2(dp, grid, lds, stream)
+                                      : launch_decode_mfma_tok_w8_128_4(dp, grid, lds, stream);
+      return maxb <= 2 ? launch_decode_mfma_tok_w8_64_2(dp, grid, lds, stream)
+                       : launch_decode_mfma_tok_w8_64_4(dp, grid, lds, stream);
+    }
+    if (hd == 128) return maxb <= 2 ? launch_decode_mfma_w8_128_2(dp, grid, lds, stream)
+                                    : launch_decode_mfma_w8_128_4(dp, grid, lds, stream);
+    return maxb <= 2 ? launch_decode_mfma_w8_64_2(dp, grid, lds, stream)
+                     : launch_decode_mfma_w8_64_4(dp, grid, lds, stream);
+  }
   if (tok) {
     if (hd == 128) {
       if (maxb <= 2) return launch_decode_mfma_tok_128_2(dp, grid, lds, stream);

@@ -204,3 +204,47 @@ def test_wide_ranges_stay_finite(gpu, kb, vb, case):
     assert np.isfinite(fast).all(), "the MFMA path overflowed"
     scale = max(1.0, float(np.abs(deq_v).max()))
     np.testing.assert_allclose(fast, want, atol=2e-3 * scale, rtol=1e-2)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("kind,kb,vb", [("kivi", 2, 2), ("kivi", 2, 4), ("kivi", 4, 4),
+                                        ("token", 2, 2), ("token", 4, 2), ("token", 4, 4)])
+def test_eight_wave_workgroups(gpu, hd, kind, kb, vb):
+    """Launches of at most one workgroup per CU with long chunks run eight waves per
+    workgroup (two per SIMD): one chunk per row here, 8.5 groups per wave, ragged rows and a
+    tail inside a group, against the four-wave kernel and the oracle."""
+    import os
+    from phasekv_amd import decode as dec
+    from phasekv_amd.kernels.packing import quantize_pack
+    print(f"case hd={hd} {kind} bits={kb},{vb}", flush=True)
+    g = torch.Generator().manual_seed(hd + 7 * kb + vb + (50 if kind == "token" else 0))
+    B, hq, hkv, S = 2, 28, 4, 2170
+    q = torch.randn(B, hq, hd, generator=g).to(torch.float16)
+    kd = torch.randn(B, hkv, S, hd, generator=g).to(torch.float16)
+    vd = torch.randn(B, hkv, S, hd, generator=g).to(torch.float16)
+    k_axis = -2 if kind == "kivi" else -1
+    pk = quantize_pack(kd.to(gpu), kb, k_axis, 32)
+    pv = quantize_pack(vd.to(gpu), vb, -1, 32)
+    # ragged rows for per-token K only: a KIVI row cut inside a K group would need the
+    # oracle to quantize that group over the tokens beyond the row's length as well
+    lens = [S, 1517] if kind == "token" else [S, S]
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    seg = dec.packed_segment(pk, pv, batched=True, splits=1, seq_lens=seq_lens)
+    outs = {}
+    for w8 in ("1", "0"):
+        os.environ["PK_WAVES8"] = w8
+        try:
+            outs[w8] = dec.fused_decode(dec.Problem(q.to(gpu), [seg], hq, require_mfma=True))
+        finally:
+            os.environ.pop("PK_WAVES8", None)
+    torch.cuda.synchronize()
+    for b, L in enumerate(lens):
+        kq = po.quantize_pack(kd[b, :, :L].float().numpy(), kb, k_axis, 32)
+        vq = po.quantize_pack(vd[b, :, :L].float().numpy(), vb, -1, 32)
+        want = ao.merge_partials([ao.segment_partial(q[b].numpy(), kq, vq, hq)], out_dtype=None)
+        for w8, out in outs.items():
+            err = np.abs(out[b].float().cpu().numpy() - want).max()
+            print(f"  row {b} waves8={w8} max abs err {err:.2e}", flush=True)
+            np.testing.assert_allclose(out[b].float().cpu().numpy(), want, atol=2e-3, rtol=1e-2)
+    np.testing.assert_allclose(outs["1"].float().cpu().numpy(), outs["0"].float().cpu().numpy(),
+                               atol=1e-3, rtol=1e-2)
