@@ -110,3 +110,73 @@ def test_llama_adapter_matches_the_dense_cache(gpu):
     cos, rel = _close(phasekv_step(model, chunk, cache),
                       model(chunk, past_key_values=dense, use_cache=True).logits[:, -1])
     assert cos > 0.999 and rel < 0.05 and len(cache.layer_tiers(0).cold) == 1
+
+
+def _np_packed(pt):
+    from oracle import packing_oracle as po
+    return po.PackedArrays(pt.packed.cpu().numpy(), pt.scale.cpu().numpy(), pt.mins.cpu().numpy(),
+                           pt.bits, pt.axis, pt.group_size, tuple(pt.orig_shape), pt.axis_len)
+
+
+def _tier_arrays(tiers, hot_rows=None):
+    """The layer's tiers as they stand, copied to the host (hot window cut at ``hot_rows``)."""
+    from oracle import attention_oracle as ao
+    seg = lambda s: ao.SegmentArrays(_np_packed(s.key), _np_packed(s.value))
+    hk, hv = tiers.hot_views()
+    if hot_rows is not None:
+        hk, hv = tiers.hot_k[:, :, :hot_rows], tiers.hot_v[:, :, :hot_rows]
+    return ao.LayerTiersArrays(seg(tiers.prompt), [seg(s) for s in tiers.prompt_extensions],
+                               [seg(s) for s in tiers.cold], hk.cpu().numpy(), hv.cpu().numpy())
+
+
+@torch.no_grad()
+def test_adapter_attention_matches_the_oracle_on_its_own_tiers(gpu, monkeypatch):
+    """Every attention call the adapter makes in a recorded step, against the float64 oracle
+    over the same packed tiers and the same q, at the decode bar (max-abs 2e-3, relative
+    1e-2): decode steps before and after a cooling, in both layers, and an input chunk
+    (each chunk token against the tiers as they stand after its append)."""
+    from oracle import attention_oracle as ao
+    from phasekv_amd import qwen2_attention as qa
+    model = _model(gpu)
+    qa.install_qwen2_phasekv_attention(model)
+    hq = model.config.num_attention_heads
+    record = {"on": False, "decode": [], "chunk": []}
+    decode, chunk = qa.fused_phasekv_decode, qa.fused_phasekv_prompt_chunk_attention
+
+    def rec_decode(q, tiers, h, **kw):
+        out = decode(q, tiers, h, **kw)
+        if record["on"]:
+            record["decode"].append((q.cpu().numpy(), _tier_arrays(tiers), out.float().cpu().numpy()))
+        return out
+
+    def rec_chunk(q, tiers, h, **kw):
+        out = chunk(q, tiers, h, **kw)
+        if record["on"]:
+            T = q.shape[0]
+            start = tiers.hot_len - T
+            record["chunk"].append((q.cpu().numpy(), [_tier_arrays(tiers, start + t + 1)
+                                                      for t in range(T)], out.float().cpu().numpy()))
+        return out
+
+    monkeypatch.setattr(qa, "fused_phasekv_decode", rec_decode)
+    monkeypatch.setattr(qa, "fused_phasekv_prompt_chunk_attention", rec_chunk)
+    g = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, 2000, (1, 300), generator=g).to(gpu)
+    first, cache = qa.phasekv_prefill(model, prompt, prompt_bits=2, cold_bits=4,
+                                      recent_window=32, lazy_g=16)
+    tok = first.argmax(-1, keepdim=True)
+    recorded = (0, 1, 47, 48, 49, 59)
+    for step in range(60):
+        record["on"] = step in recorded
+        tok = qa.phasekv_step(model, tok, cache).argmax(-1, keepdim=True)
+    assert len(cache.layer_tiers(0).cold) == 1     # a cooling happened between the records
+    record["on"] = True
+    qa.phasekv_step(model, torch.randint(0, 2000, (1, 11), generator=g).to(gpu), cache)
+    assert len(record["decode"]) == 2 * len(recorded) and len(record["chunk"]) == 2
+    for i, (q, tiers, got) in enumerate(record["decode"]):
+        want = ao.layer_tiers_attention(q, tiers, hq)
+        np.testing.assert_allclose(got, want, atol=2e-3, rtol=1e-2, err_msg=f"decode call {i}")
+    for i, (q, per_token, got) in enumerate(record["chunk"]):
+        want = np.stack([ao.layer_tiers_attention(q[t], per_token[t], hq)
+                         for t in range(q.shape[0])])
+        np.testing.assert_allclose(got, want, atol=2e-3, rtol=1e-2, err_msg=f"chunk call {i}")
