@@ -95,7 +95,9 @@ struct DecodeParams {
 // MFMA fast path (pk_decode_mfma.hip): same parameters and partial layout.  waves: 4, or 8
 // for a launch whose segments all take the wave-private group path (no device table,
 // codes up to 4 bits).
+// wave_only: every segment takes the wave-private group path (no workgroup stages, no
+// device table), so the smaller wave-path-only variant serves the launch.
 int launch_decode_mfma(const DecodeParams& dp, int lchunks, int max_kbits, int max_vbits,
-                       int waves, hipStream_t stream);
+                       int waves, bool wave_only, hipStream_t stream);
 
 }  // namespace pk

@@ -759,7 +759,8 @@ static int launch_partials(const pk_decode_problem* p, const Plan& pl, char* ws,
       const char* w8 = getenv("PK_WAVES8");   // "0": four waves always, for experiments
       const int waves = (wgs <= device_cu_count() && max_groups >= 8 && wave_path_only(p) &&
                          !(w8 && w8[0] == '0')) ? 8 : 4;
-      rc = launch_decode_mfma(dp, lchunks, pl.max_kbits, pl.max_vbits, waves, stream);
+      rc = launch_decode_mfma(dp, lchunks, pl.max_kbits, pl.max_vbits, waves, wave_path_only(p),
+                              stream);
     } else {
       dim3 grid(lchunks, p->num_kv_heads * pl.nslab, p->batch);
       hipLaunchKernelGGL(decode_partials_generic, grid, dim3(kThreads), lds, stream, dp);

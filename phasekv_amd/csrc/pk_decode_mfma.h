@@ -1425,9 +1425,10 @@ __device__ __forceinline__ void kivi_wave_groups(const SegDev& s, const SegOffse
 }
 
 // Stages of the chunk: t_first + i t_stride (i < nst), tokens below t_end.  NW: waves of
-// the workgroup.  The 8-wave variants take only what the wave-private groups read (the host
-// checks it); the 128-token workgroup stages need 4 waves.
-template <int HD, int KB, int VB, int MAXB, int NW>
+// the workgroup.  WO: a wave-path-only variant (every 8-wave variant, and the 4-wave ones
+// for launches that need no more), which takes only what the wave-private groups read (the
+// host checks it) and is a fraction of the code; the 128-token workgroup stages need 4 waves.
+template <int HD, int KB, int VB, int MAXB, int NW, bool WO>
 __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o, int t_first,
                                            int t_stride, int nst, int t_end, int wave, int lane,
                                            int tid, char* lds, int stage_bytes,
@@ -1452,13 +1453,14 @@ __device__ __forceinline__ void kivi_chunk(const SegDev& s, const SegOffsets& o,
   kl.kmeta4 = !s.kmeta_gm && (kl.row_groups % 4 == 0) && (t_first % kStage == 0) &&
               (t_stride % kStage == 0) && meta8;
   if constexpr (KB <= 4 && VB <= 4) {
-    if (NW != kWaves || (kl.kdata_tm && kl.kmeta_gm && kl.row_bytes < ((int64_t)1 << 31) / HD)) {
+    if (WO || (kl.kdata_tm && kl.kmeta_gm && kl.row_bytes < ((int64_t)1 << 31) / HD)) {
       kivi_wave_groups<HD, KB, VB>(s, o, kl, t_first, t_end, wave, wave, NW, lane, lds,
                                    2 * GroupLayout<HD, KB, VB>::bytes, qb, acc, sl2, true);
       return;
     }
   }
-  if constexpr (NW == kWaves) {
+  if constexpr (!WO) {
+    static_assert(NW == kWaves, "the workgroup stages take four waves");
     if (kl.kmode == 16 && (kl.kmeta4 || kl.kmeta_gm) && kl.row_bytes < ((int64_t)1 << 31) / HD)
       kivi_stages<HD, KB, VB, MAXB, true>(s, o, kl, t_first, t_stride, nst, t_end, wave, lane, tid, lds,
                                     stage_bytes, qb, acc, sl2);
@@ -1903,10 +1905,12 @@ __device__ __forceinline__ void touch_params(const DecodeParams& p) {
 // other variant takes KIVI segments, device tables and FP16 segments.  NW: waves per
 // workgroup, 4 (two workgroups per CU) or 8 (one workgroup of two waves per SIMD, for
 // launches of at most one workgroup per CU whose segments all take the wave-private
-// group path; no device tables).
-template <int HD, int MAXB, bool TOK, int NW>
+// group path; no device tables).  WO: only the wave-private group path (no workgroup
+// stages, no device tables), for launches that need no more; the 8-wave variants are WO.
+template <int HD, int MAXB, bool TOK, int NW, bool WO>
 __global__ void __launch_bounds__(64 * NW, 8 / NW)
 decode_mfma_kernel(const DecodeParams p) {
+  static_assert(NW == kWaves || WO, "eight-wave variants take the wave path only");
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr int NB = HD / 16;
   constexpr int KS = HD / 32;
@@ -1993,7 +1997,7 @@ decode_mfma_kernel(const DecodeParams p) {
 #undef PK_TOK_CASE
     }
   } else if (s.kind == kSegTable) {
-    if constexpr (NW == kWaves)
+    if constexpr (!WO)
       vb_bits = table_entry<HD, MAXB>(s, local, b, kvh, wave, lane, lds, qb, acc, sl2);
   } else if (s.kind == PK_SEG_FP16) {
     fp16_chunk();
@@ -2013,7 +2017,7 @@ decode_mfma_kernel(const DecodeParams p) {
 #define PK_KIVI_CASE(KB_, VB_)                                                                 \
   case KB_ * 16 + VB_:                                                                         \
     if constexpr (KB_ <= MAXB && VB_ <= MAXB)                                                  \
-      kivi_chunk<HD, KB_, VB_, MAXB, NW>(s, o, kt_first, kt_stride, knst, kt_end, wave, lane, tid, lds,  \
+      kivi_chunk<HD, KB_, VB_, MAXB, NW, WO>(s, o, kt_first, kt_stride, knst, kt_end, wave, lane, tid, lds,  \
                                      p.stage_lds, qb, acc, sl2);                               \
     break;
     if (knst > 0) {
@@ -2152,9 +2156,9 @@ inline int tok_group_bytes_hd(int kb, int vb) {
 
 // The launch of one kernel variant (instantiated by one pk_decode_mfma[_tok]_<HD>_<MAXB>.hip
 // each, so that the variants compile in parallel).
-template <int HD, int MAXB, bool TOK, int NW>
+template <int HD, int MAXB, bool TOK, int NW, bool WO>
 int launch_decode_mfma_variant(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_mfma_kernel<HD, MAXB, TOK, NW>), grid, dim3(64 * NW), lds,
+  hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_mfma_kernel<HD, MAXB, TOK, NW, WO>), grid, dim3(64 * NW), lds,
                      stream, dp);
   return check_launch("decode_mfma");
 }
@@ -2164,7 +2168,8 @@ int launch_decode_mfma_variant(const DecodeParams& dp, dim3 grid, size_t lds, hi
   int launch_decode_mfma_tok_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream);
 #define PK_DECLARE_MFMA_W8_VARIANT(HD_, MB_)                                                     \
   int launch_decode_mfma_w8_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream); \
-  int launch_decode_mfma_tok_w8_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream);
+  int launch_decode_mfma_tok_w8_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream); \
+  int launch_decode_mfma_wo_##HD_##_##MB_(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream);
 PK_DECLARE_MFMA_VARIANT(64, 2)
 PK_DECLARE_MFMA_VARIANT(64, 4)
 PK_DECLARE_MFMA_VARIANT(64, 8)
@@ -2182,13 +2187,20 @@ PK_DECLARE_MFMA_W8_VARIANT(128, 4)
 
 #ifdef PK_MFMA_HD
 // one variant of the kernel per translation unit (PK_MFMA_TOK: the per-token K variant;
-// PK_MFMA_W8: eight waves per workgroup)
+// PK_MFMA_W8: eight waves per workgroup; PK_MFMA_WO: four waves, wave-private group path
+// only)
 #ifndef PK_MFMA_W8
 #define PK_MFMA_W8 0
 #endif
+#ifndef PK_MFMA_WO
+#define PK_MFMA_WO 0
+#endif
 namespace pk {
 #define PK_CAT3(a, b, c) a##b##_##c
-#if defined(PK_MFMA_TOK) && PK_MFMA_W8
+#if PK_MFMA_WO
+#define PK_VARIANT_NAME(HD_, MB_) PK_CAT3(launch_decode_mfma_wo_, HD_, MB_)
+#define PK_VARIANT_TOK false
+#elif defined(PK_MFMA_TOK) && PK_MFMA_W8
 #define PK_VARIANT_NAME(HD_, MB_) PK_CAT3(launch_decode_mfma_tok_w8_, HD_, MB_)
 #define PK_VARIANT_TOK true
 #elif defined(PK_MFMA_TOK)
@@ -2204,7 +2216,8 @@ namespace pk {
 int PK_VARIANT_NAME(PK_MFMA_HD, PK_MFMA_MAXB)(const DecodeParams& dp, dim3 grid, size_t lds,
                                               hipStream_t stream) {
   return launch_decode_mfma_variant<PK_MFMA_HD, PK_MFMA_MAXB, PK_VARIANT_TOK,
-                                    PK_MFMA_W8 ? 8 : kWaves>(dp, grid, lds, stream);
+                                    PK_MFMA_W8 ? 8 : kWaves, PK_MFMA_W8 || PK_MFMA_WO>(
+      dp, grid, lds, stream);
 }
 #undef PK_VARIANT_TOK
 #undef PK_VARIANT_NAME

@@ -20,7 +20,7 @@ static int tok_group_bytes(int hd, int kb, int vb) {
 }
 
 int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, int max_vbits,
-                       int waves, hipStream_t stream) {
+                       int waves, bool wave_only, hipStream_t stream) {
   DecodeParams dp = dp_in;
   const int hd = dp.hd;
   // per-token K segments go to the TOK variant (the host never mixes them with KIVI
@@ -29,12 +29,14 @@ int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, in
   for (int i = 0; i < dp.nseg; ++i) tok = tok || dp.seg[i].kind == PK_SEG_TOKEN;
   const int maxb = std::max(max_kbits, max_vbits);
   const bool w8 = waves == 8 && maxb <= 4;
+  // four waves on the wave-private group path only: a fraction of the full variant's code
+  const bool wo = !w8 && !tok && wave_only && maxb <= 4;
   const size_t nw = w8 ? 8 : kWaves;
   size_t staging;
   if (tok) {
     dp.stage_lds = 0;
     staging = nw * 2 * tok_group_bytes(hd, max_kbits, max_vbits);
-  } else if (w8) {
+  } else if (w8 || wo) {
     dp.stage_lds = 0;
     staging = nw * 2 * kivi_group_bytes(hd, max_kbits, max_vbits);
   } else {
@@ -56,6 +58,12 @@ int launch_decode_mfma(const DecodeParams& dp_in, int lchunks, int max_kbits, in
                                     : launch_decode_mfma_w8_128_4(dp, grid, lds, stream);
     return maxb <= 2 ? launch_decode_mfma_w8_64_2(dp, grid, lds, stream)
                      : launch_decode_mfma_w8_64_4(dp, grid, lds, stream);
+  }
+  if (wo) {
+    if (hd == 128) return maxb <= 2 ? launch_decode_mfma_wo_128_2(dp, grid, lds, stream)
+                                    : launch_decode_mfma_wo_128_4(dp, grid, lds, stream);
+    return maxb <= 2 ? launch_decode_mfma_wo_64_2(dp, grid, lds, stream)
+                     : launch_decode_mfma_wo_64_4(dp, grid, lds, stream);
   }
   if (tok) {
     if (hd == 128) {
