@@ -471,6 +471,7 @@ static void plan_weighted(const pk_decode_problem* p, int64_t per_bh, Plan& pl) 
     row += G[i] * w[i];
   }
   const int64_t cus = device_cu_count(), slots = 2 * cus;
+  const double w8t = env_double("PK_PLAN_W8T", kPlanWave8Factor);
   std::vector<int64_t> g(ns), best_g(ns, 4);
   double best = 1e30;
   int64_t best_wgs = 0;
@@ -485,7 +486,6 @@ static void plan_weighted(const pk_decode_problem* p, int64_t per_bh, Plan& pl) 
     // and its chunks hold 8 or more groups: the groups spread over twice the waves
     int64_t gmin = INT64_MAX;
     for (int i = 0; i < ns; ++i) gmin = std::min(gmin, g[i]);
-    const double w8t = env_double("PK_PLAN_W8T", kPlanWave8Factor);
     const bool w8 = w8t > 0 && wave8 && wgs <= cus && gmin >= 8;
     auto cost = [&](int64_t groups, int64_t wi) {
       if (w8) return 5.0 + std::ceil(groups / 8.0) * (double)wi / 100.0 * w8t;
