@@ -2154,7 +2154,7 @@ inline int tok_group_bytes_hd(int kb, int vb) {
   return best;
 }
 
-// The launch of one kernel variant (instantiated by one pk_decode_mfma[_tok]_<HD>_<MAXB>.hip
+// The launch of one kernel variant (instantiated by one pk_decode_mfma[_tok][_w8|_wo]_<HD>_<MAXB>.hip
 // each, so that the variants compile in parallel).
 template <int HD, int MAXB, bool TOK, int NW, bool WO>
 int launch_decode_mfma_variant(const DecodeParams& dp, dim3 grid, size_t lds, hipStream_t stream) {

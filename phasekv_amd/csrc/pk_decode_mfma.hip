@@ -1,6 +1,7 @@
-// Launch of the MFMA decode kernel: picks the variant (per-token K or not,
-// head_dim, widest code of the launch) and sizes its LDS.  The kernel itself is
-// pk_decode_mfma.h, one variant per pk_decode_mfma[_tok]_<HD>_<MAXB>.hip.
+// Launch of the MFMA decode kernel: picks the variant (per-token K or not, head_dim,
+// widest code of the launch, four or eight waves, wave-private group path only or not)
+// and sizes its LDS.  The kernel itself is pk_decode_mfma.h, one variant per
+// pk_decode_mfma[_tok][_w8|_wo]_<HD>_<MAXB>.hip.
 #include "pk_decode_mfma.h"
 
 #include <algorithm>
