@@ -414,11 +414,14 @@ def _bench_prompt_select(device, steps, warmup, stream, with_cpu):
     attn = torch.softmax(torch.randn(1, 28, w, L, generator=gen) * 3, dim=-1).to(torch.float16)
     kw = dict(prompt_len=L, model_config=Cfg, prefill_keep_ratio=0.25, sink_tokens=4,
               obs_window=w, pool_kernel=7, pooling="maxpool")
-    dev_attn = attn.to(device)
-    sec = _time_graph([lambda: select_prompt_indices([dev_attn], **kw)], steps, warmup, stream)
     nbytes = attn.numel() * 2
+    # rotating copies of the attention rows, so that the votes read HBM as a prefill does
+    dev_attn = attn.to(device)
+    sets = [dev_attn] + [dev_attn.clone() for _ in range(_copies_for(nbytes) - 1)]
+    sec = _time_graph([lambda a=a: select_prompt_indices([a], **kw) for a in sets], steps,
+                      warmup, stream)
     res = {"config": "C4-prefill-select", "prompt_len": L, "obs_window": w, "us": sec * 1e6,
-           "votes_bytes": nbytes, "gbs": nbytes / sec / 1e9}
+           "copies": len(sets), "votes_bytes": nbytes, "gbs": nbytes / sec / 1e9}
     if with_cpu:
         from oracle import select_oracle as so
         a = attn.float().numpy()
@@ -426,7 +429,7 @@ def _bench_prompt_select(device, steps, warmup, stream, with_cpu):
         so.select_prompt_indices([a], num_kv_heads=4, **{k: v for k, v in kw.items()
                                                          if k != "model_config"})
         res["cpu_us"] = (time.perf_counter() - t0) * 1e6
-    del dev_attn
+    del dev_attn, sets
     torch.cuda.empty_cache()
     return res
 

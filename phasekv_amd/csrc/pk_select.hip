@@ -17,7 +17,7 @@
 
 namespace {
 
-constexpr int kSelThreads = 256;     // votes kernel
+constexpr int kVotesMaxWaves = 16;  // votes kernel: one wave per query head of the group, up to 16
 constexpr int kPickThreads = 1024;   // selection kernel: 16 waves share one row's candidates
 // candidates whose votes and keys are staged in LDS (8 bytes each, 144 KB)
 constexpr int64_t kMaxStagedKeys = 18 * 1024;
@@ -36,10 +36,12 @@ __device__ __forceinline__ float load_attn(const AttnView& a, int64_t off) {
 
 // votes[b, kv, j] = sum over the group's query heads g (in order) of the sum over
 // the last w query rows r (in order) of attention[b, kv * G + g, q_len - w + r, j],
-// all in float32.  A workgroup takes 64 * KPL key positions of one (b, kv): wave s
-// sums the rows of query heads s, s + 4, ... (KPL neighbouring keys per lane in one
-// load, 16 rows of loads in flight, added in row order), and wave 0 adds the heads'
-// sums in head order.
+// all in float32.  A workgroup takes 64 * KPL key positions of one (b, kv) and has one
+// wave per query head of the group (up to kVotesMaxWaves): wave s sums the rows of
+// query heads s, s + waves, ... (KPL neighbouring keys per lane in one load, 16 rows of
+// loads in flight, added in row order), and wave 0 adds the heads' sums in head order.
+// A wave per head keeps every head's rows in flight at once: the launch is bound by
+// the bytes in flight per CU.
 constexpr int kMaxGroup = 32;
 
 template <int KPL, typename T>
@@ -56,7 +58,7 @@ __device__ __forceinline__ void load_keys(const AttnView& a, int64_t off, float 
 }
 
 template <int KPL>
-__global__ void __launch_bounds__(kSelThreads)
+__global__ void __launch_bounds__(64 * kVotesMaxWaves)
 votes_kernel(AttnView a, int Hkv, int G, int64_t q_len, int64_t kv_len, int w,
              float* __restrict__ votes) {
   constexpr int TILE = 64 * KPL;
@@ -67,7 +69,7 @@ votes_kernel(AttnView a, int Hkv, int G, int64_t q_len, int64_t kv_len, int w,
   const int64_t j0 = (blockIdx.x - row * tiles) * TILE + lane * KPL;
   const int64_t b = row / Hkv, kv = row - b * Hkv;
   const int64_t jc = min(j0, kv_len - KPL);               // whole pieces stay inside the row
-  for (int g = slot; g < G; g += kSelThreads / 64) {
+  for (int g = slot; g < G; g += (int)(blockDim.x / 64)) {
     const int64_t base = b * a.sb + (kv * G + g) * a.sh + (q_len - w) * a.sq + jc * a.sk;
     float sum[KPL];
 #pragma unroll
@@ -309,14 +311,15 @@ extern "C" int pk_prompt_votes(const void* attention, int dtype, int64_t batch, 
     const int64_t blocks = batch * num_kv_heads * pk::cdiv(kv_len, 64 * kpl);
     if (blocks > 0x7fffffff) return pk::fail("attention too large");
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 threads(64 * std::min(G, kVotesMaxWaves));
     if (kpl == 4)
-      hipLaunchKernelGGL(votes_kernel<4>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+      hipLaunchKernelGGL(votes_kernel<4>, dim3((unsigned)blocks), threads, 0, s, a,
                          num_kv_heads, G, q_len, kv_len, w, votes);
     else if (kpl == 2)
-      hipLaunchKernelGGL(votes_kernel<2>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+      hipLaunchKernelGGL(votes_kernel<2>, dim3((unsigned)blocks), threads, 0, s, a,
                          num_kv_heads, G, q_len, kv_len, w, votes);
     else
-      hipLaunchKernelGGL(votes_kernel<1>, dim3((unsigned)blocks), dim3(kSelThreads), 0, s, a,
+      hipLaunchKernelGGL(votes_kernel<1>, dim3((unsigned)blocks), threads, 0, s, a,
                          num_kv_heads, G, q_len, kv_len, w, votes);
     return pk::check_launch("prompt_votes");
   });
