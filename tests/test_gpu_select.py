@@ -34,10 +34,12 @@ def test_votes_bit_exact(gpu, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("B,hq,hkv,kv", [(2, 16, 8, 4096), (1, 28, 4, 8192), (1, 6, 2, 998)])
+@pytest.mark.parametrize("B,hq,hkv,kv", [(2, 16, 8, 4096), (1, 28, 4, 8192), (1, 6, 2, 998),
+                                          (1, 4, 4, 2048), (2, 40, 2, 1024)])
 def test_votes_bit_exact_per_load_width(gpu, dtype, B, hq, hkv, kv):
     """16-bit attention takes 4 keys per lane when that gives every CU a workgroup
-    (2 x 8 kv heads x 4096 keys), else 2 (C4's 4 kv heads x 8192) or 1 (rows of 998 keys)."""
+    (2 x 8 kv heads x 4096 keys), else 2 (C4's 4 kv heads x 8192) or 1 (rows of 998 keys);
+    query heads per kv head 1 (one wave) to 20 (16 waves, some with two heads)."""
     from phasekv_amd.prompt_tier import prompt_votes
     print(f"case B={B} hq={hq} hkv={hkv} kv={kv} {dtype}", flush=True)
     a = _attn(B + kv, B, hq, 24, kv).to(dtype)
