@@ -241,6 +241,34 @@ int pk_merge_partials(const float* m, const float* l, const float* acc, int64_t 
                       int32_t n, int32_t head_dim, uint16_t* out, float* out_m,
                       float* out_l, float* out_acc, void* stream);
 
+/* One set of split partials for pk_merge_partial_sets: m, l [rows, n] and acc
+ * [rows, n, head_dim] fp32 contiguous (what pk_decode_partials writes; acc 16-byte
+ * aligned).  Output row (o, i) reads the set's row o * outer_stride + i * inner_stride,
+ * which must be < rows. */
+#define PK_MAX_PARTIAL_SETS 4
+typedef struct pk_partial_set {
+  const float* m;
+  const float* l;
+  const float* acc;
+  int64_t rows;
+  int32_t n;
+  int32_t pad_;
+  int64_t outer_stride;
+  int64_t inner_stride;
+} pk_partial_set;
+
+/* Log-sum-exp merge, per output row (o, i) of an [outer, inner] grid, of every
+ * partial of 1..PK_MAX_PARTIAL_SETS sets whose rows are numbered differently: the
+ * input-chunk attention merges its packed-tier launch (rows (head, token)) with its
+ * causal chunk launch (rows (token, head)) this way, with no transpose in between.
+ * Writes normalized fp16 out [outer, inner, head_dim] or, when out is NULL,
+ * unnormalized (m, l, acc).  The merge of _merge_partials (attention_triton.py:300-307)
+ * applied to what the reference computes with one decode call per chunk token
+ * (qwen2_attention.py:100-106); the fused chunk itself has no reference counterpart. */
+int pk_merge_partial_sets(const pk_partial_set* sets, int32_t nsets, int64_t outer,
+                          int64_t inner, int32_t head_dim, uint16_t* out, float* out_m,
+                          float* out_l, float* out_acc, void* stream);
+
 /* ---- FP16 hot window lifecycle (src/phasekv/phasekv_cache.py) -------------- */
 
 /* Largest number of hot tokens one cooling step can take. */

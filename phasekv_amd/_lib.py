@@ -28,6 +28,7 @@ PK_SEG_FP16 = 2
 
 PK_MAX_SEGMENTS_PER_LAUNCH = 8
 PK_NOALLOC_SCRATCH_BYTES = 16 << 20
+PK_MAX_PARTIAL_SETS = 4
 PK_FLAG_GENERIC_KERNEL = 1
 PK_FLAG_REQUIRE_MFMA = 2
 
@@ -74,6 +75,15 @@ class PkDecodeProblem(ctypes.Structure):
     ]
 
 
+
+class PkPartialSet(ctypes.Structure):
+    """Mirror of ``pk_partial_set``."""
+
+    _fields_ = [
+        ("m", _c_vp), ("l", _c_vp), ("acc", _c_vp), ("rows", _c_i64), ("n", _c_i32),
+        ("pad_", _c_i32), ("outer_stride", _c_i64), ("inner_stride", _c_i64),
+    ]
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     "pk_last_error": (ctypes.c_char_p, []),
@@ -109,6 +119,8 @@ _SIGNATURES = {
     "pk_fused_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(PkDecodeProblem), _c_vp, _c_vp]),
     "pk_merge_partials": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32, _c_vp,
                                          _c_vp, _c_vp, _c_vp, _c_vp]),
+    "pk_merge_partial_sets": (ctypes.c_int, [ctypes.POINTER(PkPartialSet), _c_i32, _c_i64,
+                                             _c_i64, _c_i32, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "pk_append_hot": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,
                                      _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_int, _c_i64, _c_i64, _c_vp]),

@@ -10,6 +10,7 @@ constexpr int kMaxSeg = PK_MAX_SEGMENTS_PER_LAUNCH;
 constexpr int kCombineMaxHd = 256;            // largest head_dim handled by the combine
 constexpr int kCombineLoads = 8;             // partials in flight per combine thread
 constexpr int kCombineTarget = 4;            // partials per combine thread the host aims at
+constexpr int kCombineRowsThreads = 128;     // threads per workgroup of the many-rows combine
 constexpr int kMinChunk = 64;                 // auto chunk lengths are multiples of this
 
 constexpr uint32_t kXcds = 8;                 // accelerator complex dies of an MI355X

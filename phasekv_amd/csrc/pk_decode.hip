@@ -283,6 +283,146 @@ combine_kernel(const float* __restrict__ m, const float* __restrict__ l,
   }
 }
 
+// The same merge for many rows with few partials (C <= kCombineLoads: the
+// batched decodes, hundreds of rows of eight partials, and the input-chunk
+// attention, thousands of rows of two to four).  There a workgroup per row slice is thousands of short
+// workgroups, each a load, two barriers and a store, and the launch is bound by
+// the rate at which waves start, not by the bytes.  Here one thread owns four
+// channels of one row and holds every partial of the row in registers: one
+// round trip, no barrier, one float4 load per partial.
+__global__ void __launch_bounds__(kCombineRowsThreads)
+combine_rows_kernel(const float* __restrict__ m, const float* __restrict__ l,
+                    const float* __restrict__ acc, int64_t rows, int C, int hd,
+                    uint16_t* out, float* om, float* ol, float* oacc) {
+  const int quads = hd / 4;
+  const int64_t t = (int64_t)blockIdx.x * kCombineRowsThreads + threadIdx.x;
+  const int64_t row = t / quads;
+  if (row >= rows) return;
+  const int d = (int)(t % quads) * 4;
+  const float* mr = m + row * C;
+  const float* lr = l + row * C;
+  const float* ar = acc + row * (int64_t)C * hd + d;
+  float4 a[kCombineLoads];
+  float mk[kCombineLoads], lk[kCombineLoads];
+#pragma unroll
+  for (int k = 0; k < kCombineLoads; ++k) {
+    const bool ok = k < C;
+    a[k] = ok ? *reinterpret_cast<const float4*>(ar + (int64_t)k * hd) : make_float4(0, 0, 0, 0);
+    mk[k] = ok ? mr[k] : -INFINITY;
+    lk[k] = ok ? lr[k] : 0.f;
+  }
+  float M = mk[0];
+#pragma unroll
+  for (int k = 1; k < kCombineLoads; ++k) M = fmaxf(M, mk[k]);
+  float4 S = make_float4(0, 0, 0, 0);
+  float L = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int k = 0; k < kCombineLoads; ++k) {
+      const float w = (mk[k] == -INFINITY) ? 0.f : expf(mk[k] - M);
+      S.x += w * a[k].x;
+      S.y += w * a[k].y;
+      S.z += w * a[k].z;
+      S.w += w * a[k].w;
+      L += w * lk[k];
+    }
+  }
+  const int64_t o = row * hd + d;
+  if (out) {
+    out[o] = pk_f2h(S.x / L);
+    out[o + 1] = pk_f2h(S.y / L);
+    out[o + 2] = pk_f2h(S.z / L);
+    out[o + 3] = pk_f2h(S.w / L);
+  }
+  if (oacc) *reinterpret_cast<float4*>(oacc + o) = S;
+  if (om && d == 0) {
+    om[row] = M;
+    ol[row] = L;
+  }
+}
+
+// The merge over several sets of partials whose rows are numbered differently:
+// output row (o, i) takes row o * so + i * si of every set.  One thread owns
+// four channels of one output row and folds the partials in, kCombineLoads at a
+// time, with the running maximum rescaled as in combine_kernel.
+struct PartialSetDev {
+  const float* m;
+  const float* l;
+  const float* acc;
+  int64_t so, si;
+  int n;
+};
+struct PartialSets {
+  PartialSetDev s[PK_MAX_PARTIAL_SETS];
+  int nsets;
+};
+
+__global__ void __launch_bounds__(kCombineRowsThreads)
+combine_sets_kernel(const PartialSets ps, int64_t outer, int64_t inner, int hd, uint16_t* out,
+                    float* om, float* ol, float* oacc) {
+  const int quads = hd / 4;
+  const int64_t t = (int64_t)blockIdx.x * kCombineRowsThreads + threadIdx.x;
+  const int64_t row = t / quads;
+  if (row >= outer * inner) return;
+  const int d = (int)(t % quads) * 4;
+  const int64_t o = row / inner, i = row - o * inner;
+  float M = -INFINITY, L = 0.f;
+  float4 S = make_float4(0, 0, 0, 0);
+  for (int k = 0; k < ps.nsets; ++k) {
+    const PartialSetDev& st = ps.s[k];
+    const int64_t r = o * st.so + i * st.si;
+    const float* mr = st.m + r * st.n;
+    const float* lr = st.l + r * st.n;
+    const float* ar = st.acc + r * (int64_t)st.n * hd + d;
+    for (int base = 0; base < st.n; base += kCombineLoads) {
+      float4 a[kCombineLoads];
+      float mk[kCombineLoads], lk[kCombineLoads];
+#pragma unroll
+      for (int j = 0; j < kCombineLoads; ++j) {
+        const int c = base + j;
+        const bool ok = c < st.n;
+        a[j] = ok ? *reinterpret_cast<const float4*>(ar + (int64_t)c * hd)
+                  : make_float4(0, 0, 0, 0);
+        mk[j] = ok ? mr[c] : -INFINITY;
+        lk[j] = ok ? lr[c] : 0.f;
+      }
+      float mx = mk[0];
+#pragma unroll
+      for (int j = 1; j < kCombineLoads; ++j) mx = fmaxf(mx, mk[j]);
+      const float Mn = fmaxf(M, mx);
+      if (Mn == -INFINITY) continue;
+      const float so = (M == -INFINITY) ? 0.f : expf(M - Mn);
+      S.x *= so;
+      S.y *= so;
+      S.z *= so;
+      S.w *= so;
+      L *= so;
+#pragma unroll
+      for (int j = 0; j < kCombineLoads; ++j) {
+        const float w = (mk[j] == -INFINITY) ? 0.f : expf(mk[j] - Mn);
+        S.x += w * a[j].x;
+        S.y += w * a[j].y;
+        S.z += w * a[j].z;
+        S.w += w * a[j].w;
+        L += w * lk[j];
+      }
+      M = Mn;
+    }
+  }
+  const int64_t off = row * hd + d;
+  if (out) {
+    out[off] = pk_f2h(S.x / L);
+    out[off + 1] = pk_f2h(S.y / L);
+    out[off + 2] = pk_f2h(S.z / L);
+    out[off + 3] = pk_f2h(S.w / L);
+  }
+  if (oacc) *reinterpret_cast<float4*>(oacc + off) = S;
+  if (om && d == 0) {
+    om[row] = M;
+    ol[row] = L;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host-side planning
 // ---------------------------------------------------------------------------
@@ -888,6 +1028,18 @@ static int launch_combine(const float* m, const float* l, const float* acc, int6
                           int hd, uint16_t* out, float* om, float* ol, float* oacc,
                           hipStream_t stream, const char* what) {
   if (rows == 0) return PK_OK;
+  const bool vec = hd % 4 == 0 && aligned(acc, 16) && (!oacc || aligned(oacc, 16));
+  const char* force = getenv("PK_COMBINE_ROWS");   // "0" / "1": force a kernel, for experiments
+  // one round trip per thread: few partials per row (measured on MI355X: 4.3 -> 2.9 us
+  // at 448 rows of 8, 25.5 -> 3 us at 7168 rows of 3; no gain at 896 rows of 10)
+  const bool by_rows = (force && *force) ? atoi(force) != 0 : true;
+  if (vec && by_rows && C <= kCombineLoads) {
+    const int64_t blocks = (rows * (hd / 4) + kCombineRowsThreads - 1) / kCombineRowsThreads;
+    if (blocks > INT32_MAX) return fail("too many output rows");
+    hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)blocks), dim3(kCombineRowsThreads), 0,
+                       stream, m, l, acc, rows, C, hd, out, om, ol, oacc);
+    return check_launch(what);
+  }
   // about kCombineTarget partials per thread, at least 4 and at most 16 partial lanes
   int ncs = 4;
   while (ncs < 16 && ncs * kCombineTarget < C) ncs <<= 1;
@@ -1015,5 +1167,42 @@ extern "C" int pk_merge_partials(const float* m, const float* l, const float* ac
     if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
     return launch_combine(m, l, acc, rows, n, head_dim, out, out_m, out_l, out_acc,
                           static_cast<hipStream_t>(stream), "merge_partials");
+  });
+}
+
+extern "C" int pk_merge_partial_sets(const pk_partial_set* sets, int32_t nsets, int64_t outer,
+                                     int64_t inner, int32_t head_dim, uint16_t* out,
+                                     float* out_m, float* out_l, float* out_acc, void* stream) {
+  return pk::guarded("pk_merge_partial_sets", [&]() -> int {
+    clear_error();
+    if (!sets || nsets < 1 || nsets > PK_MAX_PARTIAL_SETS)
+      return fail("between 1 and PK_MAX_PARTIAL_SETS partial sets");
+    if (outer < 0 || inner < 0) return fail("outer and inner must be >= 0");
+    if (head_dim <= 0 || head_dim > kCombineMaxHd || (head_dim & (head_dim - 1)) || head_dim < 4)
+      return fail("head_dim must be a power of two in [4, 256]");
+    if (!out && !(out_m && out_l && out_acc)) return fail("no output requested");
+    if (out_acc && !aligned(out_acc, 16)) return fail("out_acc must be 16-byte aligned");
+    PartialSets ps{};
+    ps.nsets = nsets;
+    for (int k = 0; k < nsets; ++k) {
+      const pk_partial_set& s = sets[k];
+      if (!s.m || !s.l || !s.acc) return fail("null partials");
+      if (!aligned(s.acc, 16)) return fail("partial acc must be 16-byte aligned");
+      if (s.n <= 0 || s.rows < 0 || s.outer_stride < 0 || s.inner_stride < 0)
+        return fail("partial sets need n > 0 and non-negative rows and strides");
+      if (outer && inner) {
+        const int64_t last = (outer - 1) * s.outer_stride + (inner - 1) * s.inner_stride;
+        if (last >= s.rows) return fail("a partial set's strides reach past its rows");
+      }
+      ps.s[k] = PartialSetDev{s.m, s.l, s.acc, s.outer_stride, s.inner_stride, s.n};
+    }
+    const int64_t rows = outer * inner;
+    if (rows == 0) return PK_OK;
+    const int64_t blocks = (rows * (head_dim / 4) + kCombineRowsThreads - 1) / kCombineRowsThreads;
+    if (blocks > INT32_MAX) return fail("too many output rows");
+    hipLaunchKernelGGL(combine_sets_kernel, dim3((unsigned)blocks), dim3(kCombineRowsThreads), 0,
+                       static_cast<hipStream_t>(stream), ps, outer, inner, head_dim, out, out_m,
+                       out_l, out_acc);
+    return check_launch("merge_partial_sets");
   });
 }

@@ -377,6 +377,50 @@ def decode_mlacc(problem: Problem):
     return m, l, acc
 
 
+def merge_partial_sets(sets, outer: int, inner: int, normalize: bool = True):
+    """Log-sum-exp merge of every partial of several sets per output row (o, i).
+
+    ``sets`` holds ``((m, l, acc), outer_stride, inner_stride)`` with m, l ``[rows, n]``
+    and acc ``[rows, n, hd]`` fp32 contiguous (as :func:`decode_partials` returns
+    them); output row (o, i) reads row ``o * outer_stride + i * inner_stride`` of each
+    set.  Returns fp16 ``[outer, inner, hd]``, or unnormalized (m, l, acc) of
+    ``[outer * inner]`` rows when ``normalize`` is False.
+    """
+    if not 1 <= len(sets) <= _lib.PK_MAX_PARTIAL_SETS:
+        raise ValueError(f"between 1 and {_lib.PK_MAX_PARTIAL_SETS} partial sets")
+    arr = (_lib.PkPartialSet * len(sets))()
+    keep, hd = [], None
+    for k, ((m, l, acc), so, si) in enumerate(sets):
+        _lib.require_device(m, l, acc)
+        if m.dtype != torch.float32 or l.dtype != torch.float32 or acc.dtype != torch.float32:
+            raise ValueError("partials must be float32")
+        if m.dim() != 2 or l.shape != m.shape or acc.dim() != 3 or acc.shape[:2] != m.shape:
+            raise ValueError("partials must be m, l [rows, n] and acc [rows, n, hd]")
+        if not (m.is_contiguous() and l.is_contiguous() and acc.is_contiguous()):
+            raise ValueError("partials must be contiguous")
+        if hd is not None and acc.shape[2] != hd:
+            raise ValueError("every set must have the same head_dim")
+        hd = acc.shape[2]
+        keep += [m, l, acc]
+        arr[k] = _lib.PkPartialSet(m.data_ptr(), l.data_ptr(), acc.data_ptr(), m.shape[0],
+                                   m.shape[1], 0, so, si)
+    dev = _lib.require_device(*keep)
+    lib = _lib.load()
+    stream = _lib.stream_ptr(dev)
+    if normalize:
+        out = torch.empty(outer, inner, hd, dtype=torch.float16, device=dev)
+        _lib.check(lib.pk_merge_partial_sets(arr, len(sets), outer, inner, hd, out.data_ptr(),
+                                             None, None, None, stream), "merge_partial_sets")
+        return out
+    om = torch.empty(outer * inner, dtype=torch.float32, device=dev)
+    ol = torch.empty(outer * inner, dtype=torch.float32, device=dev)
+    oacc = torch.empty(outer * inner, hd, dtype=torch.float32, device=dev)
+    _lib.check(lib.pk_merge_partial_sets(arr, len(sets), outer, inner, hd, None, om.data_ptr(),
+                                         ol.data_ptr(), oacc.data_ptr(), stream),
+               "merge_partial_sets")
+    return om, ol, oacc
+
+
 def merge_partials(m: torch.Tensor, l: torch.Tensor, acc: torch.Tensor, normalize: bool):
     """Log-sum-exp merge over dim 1 of m, l [rows, n] and acc [rows, n, hd] (fp32)."""
     dev = _lib.require_device(m, l, acc)

@@ -353,6 +353,12 @@ def fused_phasekv_decode_batched(q: torch.Tensor, tiers, num_attention_heads: in
                                              prompt_lens=prompt_lens))
 
 
+# Chunk tokens x context tokens x Hkv x hd from which the input-chunk attention runs
+# the packed tiers once with the chunk's queries as heads rather than once per query
+# token (the two methods' measured crossover on MI355X lies between 1.5e8 and 2.2e8).
+CHUNK_HEADS_MIN_WORK = 160_000_000
+
+
 def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_heads: int,
                                          method: str = "auto") -> torch.Tensor:
     """Causal attention of a whole input chunk over the packed cache, in one pass.
@@ -364,16 +370,19 @@ def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_h
     chunk token (``qwen2_attention.py:100-106``, ``phasekv_cache.py:344-371``).
     Returns ``[T, Hq, hd]`` fp16.
 
-    ``method="heads"``: two decode launches and one merge.  The T queries ride as
+    ``method="heads"``: two partial launches and one merge.  The T queries ride as
     ``T * Hq`` heads (head ``(kv, g, t)``) over the packed segments and the pre-chunk
     hot rows, so each KV chunk is read once per 16 query rows; the chunk's own rows are
     a batch of T over one broadcast segment with ``t + 1`` valid rows for query t; the
-    two unnormalized partials per query row are merged by log-sum-exp.
+    two launches' split partials are merged in one pass.
     ``method="batch"``: one decode launch with the T queries as a batch of T over
     broadcast segments (every tier read once per query token, mostly from the caches)
     and the whole window with ``start + t + 1`` valid rows for query t: fewer launches,
-    more reads.  ``"auto"`` takes ``"batch"``, measured faster at every chunk length
-    from 4 to 256 tokens on MI355X (the repeated reads come from L2 and the MALL).
+    more reads.  ``"auto"`` takes ``"heads"`` once T * context tokens * Hkv * hd reaches
+    ``CHUNK_HEADS_MIN_WORK``, else ``"batch"`` (measured on MI355X: at 4.5K context
+    tokens, Hkv 4, hd 128 the two tie at T = 64 and heads is 1.5x faster at T = 256;
+    at 33K tokens heads wins from T = 16, 1.9x at T = 256; at 544 tokens, Hkv 2, hd 64
+    batch wins at every T up to 256).
     """
     if method not in ("auto", "heads", "batch"):
         raise ValueError("method must be auto, heads or batch")
@@ -388,7 +397,12 @@ def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_h
     if hot_k.shape[0] != 1:
         raise ValueError("the PhaseKV prompt chunk path takes batch = 1")
     start = hot_len - T
-    if method in ("batch", "auto"):
+    if method == "auto":
+        context = hot_len + sum(seg.key.orig_shape[-2] for seg in
+                                [tiers.prompt, *tiers.prompt_extensions, *tiers.cold])
+        work = T * context * hot_k.shape[1] * hd
+        method = "heads" if work >= CHUNK_HEADS_MIN_WORK else "batch"
+    if method == "batch":
         packed = [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]
         segs = [_dec.packed_segment(_remove_batch(seg.key), _remove_batch(seg.value),
                                     batched=False, broadcast=T)
@@ -400,27 +414,23 @@ def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_h
         cold.append(False)
         return _dec.fused_decode(_with_table(q.contiguous(), segs, cold, hq))
     # (a) packed tiers and the pre-chunk hot rows, the T queries as heads (kv, g, t)
-    segs = []
-    for segment in [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]:
-        segs.append(_dec.packed_segment(_remove_batch(segment.key), _remove_batch(segment.value),
-                                        batched=False))
+    packed = [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]
+    segs = [_dec.packed_segment(_remove_batch(seg.key), _remove_batch(seg.value), batched=False)
+            for seg in packed]
+    cold = [i > len(tiers.prompt_extensions) for i in range(len(packed))]
     if start:
         segs.append(_dec.fp16_segment(hot_k[0, :, :start], hot_v[0, :, :start], batched=False))
+        cold.append(False)
     q_heads = q.permute(1, 0, 2).reshape(1, hq * T, hd)
-    ma, la, acca = _dec.decode_mlacc(_dec.Problem(q_heads, segs, hq * T))
+    part_a = _dec.decode_partials(_with_table(q_heads, segs, cold, hq * T))
     # (b) the chunk's own rows, causal: query t sees rows start .. start + t
     lens = torch.arange(1, T + 1, dtype=torch.int32, device=q.device)
     chunk = _dec.fp16_segment(hot_k[0, :, start:], hot_v[0, :, start:], batched=False,
                               seq_lens=lens, broadcast=T)
-    mb, lb, accb = _dec.decode_mlacc(_dec.Problem(q, [chunk], hq))
-    # rows of (a) in (t, h) order, then the merge
-    ma = ma.view(hq, T).t()
-    la = la.view(hq, T).t()
-    acca = acca.view(hq, T, hd).permute(1, 0, 2)
-    m = torch.stack((ma.reshape(-1), mb), dim=1)
-    l = torch.stack((la.reshape(-1), lb), dim=1)
-    acc = torch.stack((acca.reshape(-1, hd), accb), dim=1)
-    return _dec.merge_partials(m, l, acc, normalize=True).view(T, hq, hd)
+    part_b = _dec.decode_partials(_dec.Problem(q, [chunk], hq))
+    # one merge of both launches' partials: output row (t, h) is row h * T + t of (a)
+    # and row t * hq + h of (b)
+    return _dec.merge_partial_sets([(part_a, 1, T), (part_b, hq, 1)], T, hq)
 
 
 def dense_fp16_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
