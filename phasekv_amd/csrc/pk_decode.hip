@@ -196,10 +196,12 @@ decode_partials_generic(const DecodeParams p) {
 }
 
 // Log-sum-exp merge of the C partials of each output row
-// (attention_triton.py:257-266, 300-307).  A workgroup owns one row and a slice
-// of hs channels (16 <= hs <= 64, chosen by the host from C: many partials per
-// row give narrow slices, so a batch-1 decode still spreads over rows * hd / 16
-// workgroups).  Thread (cs, d) owns channel d of partials cs, cs + ncs, ...
+// (attention_triton.py:257-266, 300-307).  Three kernels share the contract; the
+// host picks by C (combine_rows_kernel for C <= 8, combine_wave_kernel for C <= 128,
+// this one for longer rows, head_dims below 16 and buffers not 16-byte aligned).
+// A workgroup owns one row and a slice of hs channels (16 <= hs <= 64, chosen by
+// the host from C: many partials per row give narrow slices, so a batch-1 decode
+// still spreads over rows * hd / 16 workgroups).  Thread (cs, d) owns channel d of partials cs, cs + ncs, ...
 // (ncs = 256 / hs): it loads m, l and acc of up to kCombineLoads of them at
 // once, so a pass is one memory round trip.  The
 // row maximum is a wave shuffle reduction plus one LDS exchange between the
@@ -327,6 +329,72 @@ combine_rows_kernel(const float* __restrict__ m, const float* __restrict__ l,
       L += w * lk[k];
     }
   }
+  const int64_t o = row * hd + d;
+  if (out) {
+    out[o] = pk_f2h(S.x / L);
+    out[o + 1] = pk_f2h(S.y / L);
+    out[o + 2] = pk_f2h(S.z / L);
+    out[o + 3] = pk_f2h(S.w / L);
+  }
+  if (oacc) *reinterpret_cast<float4*>(oacc + o) = S;
+  if (om && d == 0) {
+    om[row] = M;
+    ol[row] = L;
+  }
+}
+
+// The merge for few rows of more partials (8 < C <= 16 * NL: the batch-1 decodes,
+// 28 rows of 35 partials at C2).  One wave per (row, 16 channels): lane (cs, q)
+// holds channels 4q .. 4q + 3 of partials cs, cs + 16, ..., so the row maximum
+// and the sums are four lane exchanges, with no LDS and no barrier.
+template <int NL>
+__global__ void __launch_bounds__(64)
+combine_wave_kernel(const float* __restrict__ m, const float* __restrict__ l,
+                    const float* __restrict__ acc, int64_t rows, int C, int hd,
+                    uint16_t* out, float* om, float* ol, float* oacc) {
+  const int lane = threadIdx.x;
+  const int nsl = hd / 16;
+  const int64_t row = blockIdx.x / nsl;
+  if (row >= rows) return;
+  const int slice = (int)(blockIdx.x % nsl);
+  const int q = lane & 3, cs = lane >> 2;
+  const int d = slice * 16 + q * 4;
+  const float* mr = m + row * C;
+  const float* lr = l + row * C;
+  const float* ar = acc + row * (int64_t)C * hd + d;
+  float4 a[NL];
+  float mk[NL], lk[NL];
+#pragma unroll
+  for (int k = 0; k < NL; ++k) {
+    const int c = cs + 16 * k;
+    const bool ok = c < C;
+    a[k] = ok ? *reinterpret_cast<const float4*>(ar + (int64_t)c * hd) : make_float4(0, 0, 0, 0);
+    mk[k] = ok ? mr[c] : -INFINITY;
+    lk[k] = ok ? lr[c] : 0.f;
+  }
+  float M = mk[0];
+#pragma unroll
+  for (int k = 1; k < NL; ++k) M = fmaxf(M, mk[k]);
+  M = wave_max_over(M, 4);
+  float4 S = make_float4(0, 0, 0, 0);
+  float L = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const float w = (mk[k] == -INFINITY) ? 0.f : expf(mk[k] - M);
+      S.x += w * a[k].x;
+      S.y += w * a[k].y;
+      S.z += w * a[k].z;
+      S.w += w * a[k].w;
+      L += w * lk[k];
+    }
+  }
+  S.x = wave_sum_over(S.x, 4);
+  S.y = wave_sum_over(S.y, 4);
+  S.z = wave_sum_over(S.z, 4);
+  S.w = wave_sum_over(S.w, 4);
+  L = wave_sum_over(L, 4);
+  if (cs != 0) return;
   const int64_t o = row * hd + d;
   if (out) {
     out[o] = pk_f2h(S.x / L);
@@ -1029,15 +1097,33 @@ static int launch_combine(const float* m, const float* l, const float* acc, int6
                           hipStream_t stream, const char* what) {
   if (rows == 0) return PK_OK;
   const bool vec = hd % 4 == 0 && aligned(acc, 16) && (!oacc || aligned(oacc, 16));
-  const char* force = getenv("PK_COMBINE_ROWS");   // "0" / "1": force a kernel, for experiments
+  // "0" workgroup slices, "1" rows, "2" waves: force a kernel where it applies, for experiments
+  const char* force = getenv("PK_COMBINE_KERNEL");
+  const int kind = (force && *force) ? atoi(force) : -1;
   // one round trip per thread: few partials per row (measured on MI355X: 4.3 -> 2.9 us
   // at 448 rows of 8, 25.5 -> 3 us at 7168 rows of 3; no gain at 896 rows of 10)
-  const bool by_rows = (force && *force) ? atoi(force) != 0 : true;
-  if (vec && by_rows && C <= kCombineLoads) {
+  if (vec && (kind < 0 || kind == 1) && C <= kCombineLoads) {
     const int64_t blocks = (rows * (hd / 4) + kCombineRowsThreads - 1) / kCombineRowsThreads;
     if (blocks > INT32_MAX) return fail("too many output rows");
     hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)blocks), dim3(kCombineRowsThreads), 0,
                        stream, m, l, acc, rows, C, hd, out, om, ol, oacc);
+    return check_launch(what);
+  }
+  // one wave per (row, 16 channels): 28 rows of 35 at C2 3.46 -> 2.85 us (8 channels per
+  // wave 2.97, 4 channels 3.35, 32 channels 3.11)
+  if (vec && hd % 16 == 0 && (kind < 0 || kind == 2) && C <= 16 * kCombineLoads) {
+    const int64_t blocks = rows * (hd / 16);
+    if (blocks > INT32_MAX) return fail("too many output rows");
+    const dim3 grid((unsigned)blocks), block(64);
+    if (C <= 32)
+      hipLaunchKernelGGL(combine_wave_kernel<2>, grid, block, 0, stream, m, l, acc, rows, C,
+                         hd, out, om, ol, oacc);
+    else if (C <= 64)
+      hipLaunchKernelGGL(combine_wave_kernel<4>, grid, block, 0, stream, m, l, acc, rows, C,
+                         hd, out, om, ol, oacc);
+    else
+      hipLaunchKernelGGL(combine_wave_kernel<kCombineLoads>, grid, block, 0, stream, m, l,
+                         acc, rows, C, hd, out, om, ol, oacc);
     return check_launch(what);
   }
   // about kCombineTarget partials per thread, at least 4 and at most 16 partial lanes

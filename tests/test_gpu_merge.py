@@ -1,6 +1,6 @@
 """The log-sum-exp merges of split partials against the oracle's merge: the one-set merge
-(pk_merge_partials: few partials over many rows and many partials over few rows take
-different kernels) and the merge over sets whose rows are numbered differently
+(pk_merge_partials: up to 8, up to 128 and more partials per row, and head_dims below 16,
+take different kernels) and the merge over sets whose rows are numbered differently
 (pk_merge_partial_sets, what the input-chunk attention uses)."""
 import numpy as np
 import pytest
@@ -36,7 +36,9 @@ def _oracle(sets):
 
 @pytest.mark.parametrize("rows,n,hd", [(3000, 1, 128), (3000, 2, 128), (700, 5, 64),
                                        (448, 8, 128), (448, 10, 128), (448, 16, 128),
-                                       (280, 17, 128), (28, 35, 128), (28, 64, 64)])
+                                       (280, 17, 128), (28, 35, 128), (28, 64, 64),
+                                       (28, 65, 128), (14, 128, 64), (28, 150, 128),
+                                       (20, 40, 8)])
 def test_merge_partials_matches_the_oracle(gpu, rows, n, hd):
     from phasekv_amd import decode as dec
     print(f"case rows={rows} n={n} hd={hd}", flush=True)
