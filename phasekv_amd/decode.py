@@ -316,6 +316,10 @@ def cached_workspace(device: torch.device, nbytes: int,
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            # a buffer allocated under capture belongs to the graph's pool: keep it for
+            # this call only, so a later, larger call cannot free memory a graph reads
+            return torch.empty(nbytes, dtype=torch.uint8, device=device)
         size = max(nbytes + nbytes // 2, 4 << 20)
         ws = torch.empty(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
@@ -375,6 +379,44 @@ def decode_mlacc(problem: Problem):
     _lib.check(lib.pk_decode_combine(ctypes.byref(problem.c), ws.data_ptr(), None, m.data_ptr(),
                                      l.data_ptr(), acc.data_ptr(), stream), "decode_combine")
     return m, l, acc
+
+
+def merged_partials_decode(parts, outer: int, inner: int) -> torch.Tensor:
+    """Split partials of several decode problems, merged per output row (o, i) in one pass.
+
+    ``parts`` holds ``(problem, outer_stride, inner_stride)``: output row (o, i) reads
+    row ``o * outer_stride + i * inner_stride`` of each problem's ``B * Hq`` partial
+    rows.  The partials share the per-stream workspace (one launch per problem, then
+    ``pk_merge_partial_sets``); returns fp16 ``[outer, inner, hd]``.
+    """
+    if not 1 <= len(parts) <= _lib.PK_MAX_PARTIAL_SETS:
+        raise ValueError(f"between 1 and {_lib.PK_MAX_PARTIAL_SETS} problems")
+    dev, hd = parts[0][0].device, parts[0][0].hd
+    align = lambda x: (x + 255) & ~255
+    sizes, offs, total = [], [], 0
+    for problem, _, _ in parts:
+        if problem.device != dev or problem.hd != hd:
+            raise ValueError("the problems must share the device and head_dim")
+        nbytes, splits = problem.workspace_size()
+        sizes.append((nbytes, splits))
+        offs.append(total)
+        total = align(total + nbytes)
+    stream = _lib.stream_ptr(dev)
+    base = cached_workspace(dev, total, stream).data_ptr()
+    lib = _lib.load()
+    sets = (_lib.PkPartialSet * len(parts))()
+    for k, ((problem, so, si), (nbytes, splits), off) in enumerate(zip(parts, sizes, offs)):
+        _lib.check(lib.pk_decode_partials(ctypes.byref(problem.c), base + off, nbytes, stream),
+                   "decode_partials")
+        rows = problem.batch * problem.hq
+        off_l = align(rows * splits * 4)              # the layout decode_partials reads back
+        off_acc = align(off_l + rows * splits * 4)
+        sets[k] = _lib.PkPartialSet(base + off, base + off + off_l, base + off + off_acc, rows,
+                                    splits, 0, so, si)
+    out = torch.empty(outer, inner, hd, dtype=torch.float16, device=dev)
+    _lib.check(lib.pk_merge_partial_sets(sets, len(parts), outer, inner, hd, out.data_ptr(),
+                                         None, None, None, stream), "merge_partial_sets")
+    return out
 
 
 def merge_partial_sets(sets, outer: int, inner: int, normalize: bool = True):

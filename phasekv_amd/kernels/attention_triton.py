@@ -355,8 +355,14 @@ def fused_phasekv_decode_batched(q: torch.Tensor, tiers, num_attention_heads: in
 
 # Chunk tokens x context tokens x Hkv x hd from which the input-chunk attention runs
 # the packed tiers once with the chunk's queries as heads rather than once per query
-# token (the two methods' measured crossover on MI355X lies between 1.5e8 and 2.2e8).
+# token.  Under graph capture only GPU time counts: the two methods' measured
+# crossover on MI355X lies between 1.5e8 and 2.2e8.  An eager call also pays the heads
+# form's host work, about 35 us more than the batch form's (a second decode problem,
+# the query transpose, two more launches), while a host-bound caller's GPU time hides
+# behind its other host work: in an eager 4-layer Qwen2.5-7B-shaped model the heads
+# form lost at 1.1e9 (64 tokens over 33K) and won at 2.2e9 (128 tokens over 33K).
 CHUNK_HEADS_MIN_WORK = 160_000_000
+CHUNK_HEADS_MIN_WORK_EAGER = 1_600_000_000
 
 
 def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_heads: int,
@@ -379,10 +385,11 @@ def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_h
     broadcast segments (every tier read once per query token, mostly from the caches)
     and the whole window with ``start + t + 1`` valid rows for query t: fewer launches,
     more reads.  ``"auto"`` takes ``"heads"`` once T * context tokens * Hkv * hd reaches
-    ``CHUNK_HEADS_MIN_WORK``, else ``"batch"`` (measured on MI355X: at 4.5K context
-    tokens, Hkv 4, hd 128 the two tie at T = 64 and heads is 1.5x faster at T = 256;
-    at 33K tokens heads wins from T = 16, 1.9x at T = 256; at 544 tokens, Hkv 2, hd 64
-    batch wins at every T up to 256).
+    ``CHUNK_HEADS_MIN_WORK`` under graph capture, or ``CHUNK_HEADS_MIN_WORK_EAGER`` in an
+    eager call, else ``"batch"`` (GPU time on MI355X: at 4.5K context tokens, Hkv 4,
+    hd 128 the two tie at T = 64 and heads is 1.5x faster at T = 256; at 33K tokens
+    heads wins from T = 16, 1.9x at T = 256; at 544 tokens, Hkv 2, hd 64 batch wins at
+    every T up to 256).
     """
     if method not in ("auto", "heads", "batch"):
         raise ValueError("method must be auto, heads or batch")
@@ -401,7 +408,9 @@ def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_h
         context = hot_len + sum(seg.key.orig_shape[-2] for seg in
                                 [tiers.prompt, *tiers.prompt_extensions, *tiers.cold])
         work = T * context * hot_k.shape[1] * hd
-        method = "heads" if work >= CHUNK_HEADS_MIN_WORK else "batch"
+        bound = (CHUNK_HEADS_MIN_WORK if torch.cuda.is_current_stream_capturing()
+                 else CHUNK_HEADS_MIN_WORK_EAGER)
+        method = "heads" if work >= bound else "batch"
     if method == "batch":
         packed = [tiers.prompt, *tiers.prompt_extensions, *tiers.cold]
         segs = [_dec.packed_segment(_remove_batch(seg.key), _remove_batch(seg.value),
@@ -422,15 +431,15 @@ def fused_phasekv_prompt_chunk_attention(q: torch.Tensor, tiers, num_attention_h
         segs.append(_dec.fp16_segment(hot_k[0, :, :start], hot_v[0, :, :start], batched=False))
         cold.append(False)
     q_heads = q.permute(1, 0, 2).reshape(1, hq * T, hd)
-    part_a = _dec.decode_partials(_with_table(q_heads, segs, cold, hq * T))
+    heads = _with_table(q_heads, segs, cold, hq * T)
     # (b) the chunk's own rows, causal: query t sees rows start .. start + t
     lens = torch.arange(1, T + 1, dtype=torch.int32, device=q.device)
     chunk = _dec.fp16_segment(hot_k[0, :, start:], hot_v[0, :, start:], batched=False,
                               seq_lens=lens, broadcast=T)
-    part_b = _dec.decode_partials(_dec.Problem(q, [chunk], hq))
+    causal = _dec.Problem(q, [chunk], hq)
     # one merge of both launches' partials: output row (t, h) is row h * T + t of (a)
     # and row t * hq + h of (b)
-    return _dec.merge_partial_sets([(part_a, 1, T), (part_b, hq, 1)], T, hq)
+    return _dec.merged_partials_decode([(heads, 1, T), (causal, hq, 1)], T, hq)
 
 
 def dense_fp16_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -83,3 +83,49 @@ def test_chunk_attention_rejects_a_chunk_longer_than_the_window(gpu):
     q = torch.zeros(3, 8, 64, dtype=torch.float16, device=gpu)
     with pytest.raises(ValueError, match="last rows"):
         fused_phasekv_prompt_chunk_attention(q, cache.layer_tiers(0), 8)
+
+
+def test_chunk_attention_graph_replays_take_the_heads_form(gpu):
+    """Under graph capture ``auto`` takes the heads form from a smaller chunk than in an
+    eager call (no host cost per replay): a 128-token chunk over a 4K-token cache is
+    eager batch and captured heads.  The captured call finds the per-stream workspace
+    sized for the batch form and takes its own buffer from the graph's pool; every
+    replay, with eager work in between, matches an eager heads call bit for bit."""
+    from phasekv_amd.cache import PhaseKVCache
+    from phasekv_amd.kernels import attention_triton as at
+    g = torch.Generator().manual_seed(41)
+    hq, hkv, hd, S, T = 28, 4, 128, 4096, 128
+    k = torch.randn(1, hkv, S, hd, generator=g).to(torch.float16).to(gpu)
+    v = torch.randn(1, hkv, S, hd, generator=g).to(torch.float16).to(gpu)
+    cache = PhaseKVCache.from_dense_prefill(_Dense([k], [v]), prompt_len=S, prompt_bits=2)
+    cache.begin_prompt_chunk(T)
+    ck = torch.randn(1, hkv, T, hd, generator=g).to(torch.float16).to(gpu)
+    cv = torch.randn(1, hkv, T, hd, generator=g).to(torch.float16).to(gpu)
+    cache.append_prompt_chunk(0, ck, cv)
+    tiers = cache.layer_tiers(0)
+    context = tiers.hot_len + sum(s.key.orig_shape[-2] for s in [tiers.prompt, *tiers.cold])
+    work = T * context * hkv * hd
+    assert at.CHUNK_HEADS_MIN_WORK <= work < at.CHUNK_HEADS_MIN_WORK_EAGER
+    q = torch.randn(T, hq, hd, generator=g).to(torch.float16).to(gpu)
+    heads = at.fused_phasekv_prompt_chunk_attention(q, tiers, hq, method="heads")
+    batch = at.fused_phasekv_prompt_chunk_attention(q, tiers, hq, method="batch")
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        eager = at.fused_phasekv_prompt_chunk_attention(q, tiers, hq)     # batch, eager
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = at.fused_phasekv_prompt_chunk_attention(q, tiers, hq)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(eager, batch)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        junk = torch.randn(1 << 20, device=gpu).sum()    # eager work between replays
+        assert torch.equal(out, heads)
+        del junk
+    np.testing.assert_allclose(out.float().cpu().numpy(), batch.float().cpu().numpy(),
+                               atol=1e-3, rtol=1e-2)
+    cache.finish_prompt_chunk()
