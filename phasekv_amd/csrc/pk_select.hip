@@ -38,8 +38,9 @@ __device__ __forceinline__ float load_attn(const AttnView& a, int64_t off) {
 // the last w query rows r (in order) of attention[b, kv * G + g, q_len - w + r, j],
 // all in float32.  A workgroup takes 64 * KPL key positions of one (b, kv) and has one
 // wave per query head of the group (up to kVotesMaxWaves): wave s sums the rows of
-// query heads s, s + waves, ... (KPL neighbouring keys per lane in one load, 16 rows of
-// loads in flight, added in row order), and wave 0 adds the heads' sums in head order.
+// query heads s, s + waves, ... (KPL neighbouring keys per lane in one load, 64 / KPL
+// rows of raw 16-bit loads in flight, added in row order; 16 rows of converted loads for
+// other dtypes and tails), and wave 0 adds the heads' sums in head order.
 // A wave per head keeps every head's rows in flight at once: the launch is bound by
 // the bytes in flight per CU.
 constexpr int kMaxGroup = 32;
@@ -75,6 +76,31 @@ votes_kernel(AttnView a, int Hkv, int G, int64_t q_len, int64_t kv_len, int w,
 #pragma unroll
     for (int i = 0; i < KPL; ++i) sum[i] = 0.f;
     int r = 0;
+    if constexpr (KPL > 1) {
+      // RB rows of raw 16-bit keys in flight (64 registers), converted as they are
+      // added: the sums still run over the rows in order
+      constexpr int RB = 64 / KPL;
+      using V = uint16_t __attribute__((ext_vector_type(KPL)));
+      const bool f16 = a.dtype == PK_DTYPE_F16;
+      // the row's address is wave-uniform (scalar registers) plus this lane's 32-bit key
+      // offset, so the RB loads need no address registers of their own
+      const int gu = __builtin_amdgcn_readfirstlane(g);
+      const uint16_t* up = static_cast<const uint16_t*>(a.p) + b * a.sb + (kv * G + gu) * a.sh +
+                           (q_len - w) * a.sq;
+      const uint32_t lbytes = static_cast<uint32_t>(jc * a.sk) * 2u;
+      for (; r + RB <= w; r += RB) {
+        V x[RB];
+#pragma unroll
+        for (int u = 0; u < RB; ++u)
+          x[u] = *reinterpret_cast<const V*>(
+              reinterpret_cast<const char*>(up + (int64_t)(r + u) * a.sq) + lbytes);
+#pragma unroll
+        for (int u = 0; u < RB; ++u)
+#pragma unroll
+          for (int i = 0; i < KPL; ++i)
+            sum[i] = __fadd_rn(sum[i], f16 ? pk_h2f(x[u][i]) : pk_bf2f(x[u][i]));
+      }
+    }
     for (; r + 16 <= w; r += 16) {
       float x[16][KPL];
 #pragma unroll
