@@ -402,7 +402,8 @@ def merged_partials_decode(parts, outer: int, inner: int) -> torch.Tensor:
         offs.append(total)
         total = align(total + nbytes)
     stream = _lib.stream_ptr(dev)
-    base = cached_workspace(dev, total, stream).data_ptr()
+    ws = cached_workspace(dev, total, stream)     # held until every launch is enqueued
+    base = ws.data_ptr()
     lib = _lib.load()
     sets = (_lib.PkPartialSet * len(parts))()
     for k, ((problem, so, si), (nbytes, splits), off) in enumerate(zip(parts, sizes, offs)):
