@@ -94,3 +94,38 @@ def test_transposed_storage_only_for_the_second_innermost_axis():
                               None, 7, None)
     assert rc == _lib.PK_ERR_INVALID
 
+
+
+def test_merge_partial_sets_rejects_bad_sets_before_any_launch():
+    """pk_merge_partial_sets validates every set on the host: no launch (and so no GPU)
+    is reached by a bad call."""
+    lib = _lib.load()
+    fake = 1 << 32                                     # never dereferenced on these paths
+
+    def call(sets, nsets, outer=5, inner=8, hd=64, out=fake):
+        arr = (_lib.PkPartialSet * max(1, len(sets)))(*sets)
+        return lib.pk_merge_partial_sets(arr, nsets, outer, inner, hd, out, None, None, None,
+                                         None)
+
+    ok = _lib.PkPartialSet(fake, fake, fake, 40, 2, 0, 8, 1)       # last row 4 * 8 + 7 = 39
+    cases = [
+        ([ok], 0, {}, "partial sets"),
+        ([ok] * 5, 5, {}, "partial sets"),
+        ([ok], 1, {"hd": 48}, "head_dim"),
+        ([ok], 1, {"hd": 2}, "head_dim"),
+        ([ok], 1, {"out": None}, "no output"),
+        ([_lib.PkPartialSet(fake, fake, fake, 40, 2, 0, 1, 6)], 1, {}, "past its rows"),
+        ([_lib.PkPartialSet(fake, fake, fake, 40, 0, 0, 8, 1)], 1, {}, "n > 0"),
+        ([_lib.PkPartialSet(fake, 0, fake, 40, 2, 0, 8, 1)], 1, {}, "null partials"),
+        ([_lib.PkPartialSet(fake, fake, fake + 4, 40, 2, 0, 8, 1)], 1, {}, "16-byte aligned"),
+    ]
+    for sets, nsets, kw, msg in cases:
+        assert call(sets, nsets, **kw) == _lib.PK_ERR_INVALID, msg
+        assert msg.encode() in lib.pk_last_error(), (msg, lib.pk_last_error())
+    # and the Python wrapper refuses host tensors (no CPU path) and more than four sets
+    from phasekv_amd import decode as dec
+    m, l, acc = torch.zeros(4, 2), torch.ones(4, 2), torch.zeros(4, 2, 8)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        dec.merge_partial_sets([((m, l, acc), 1, 1)], 4, 1)
+    with pytest.raises(ValueError, match="partial sets"):
+        dec.merge_partial_sets([((m, l, acc), 1, 1)] * 5, 4, 1)
