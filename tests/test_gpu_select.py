@@ -39,12 +39,15 @@ def test_votes_bit_exact(gpu, dtype):
 def test_votes_bit_exact_per_load_width(gpu, dtype, B, hq, hkv, kv):
     """16-bit attention takes 4 keys per lane when that gives every CU a workgroup
     (2 x 8 kv heads x 4096 keys), else 2 (C4's 4 kv heads x 8192) or 1 (rows of 998 keys);
-    query heads per kv head 1 (one wave) to 20 (16 waves, some with two heads)."""
+    query heads per kv head 1 (one wave) to 20 (16 waves, some with two heads).  Windows
+    of 24, 64 and 70 rows: below, at and past the 32 (2 keys per lane) or 16 (4 keys)
+    rows of raw loads a wave keeps in flight, with a tail of converted loads."""
     from phasekv_amd.prompt_tier import prompt_votes
-    print(f"case B={B} hq={hq} hkv={hkv} kv={kv} {dtype}", flush=True)
-    a = _attn(B + kv, B, hq, 24, kv).to(dtype)
-    got = prompt_votes(a.to(gpu), hkv, 24).cpu().numpy()
-    assert np.array_equal(got, so.observation_votes(a.float().numpy(), hkv, 24))
+    a = _attn(B + kv, B, hq, 70, kv).to(dtype)
+    for w in (24, 64, 70):
+        print(f"case B={B} hq={hq} hkv={hkv} kv={kv} {dtype} w={w}", flush=True)
+        got = prompt_votes(a.to(gpu), hkv, w).cpu().numpy()
+        assert np.array_equal(got, so.observation_votes(a.float().numpy(), hkv, w)), w
 
 
 @pytest.mark.parametrize("pooling,kernel", [("maxpool", 7), ("avgpool", 7), ("maxpool", 4),
