@@ -136,8 +136,41 @@ votes_kernel(AttnView a, int Hkv, int G, int64_t q_len, int64_t kv_len, int w,
 // max pooling takes the max over c[j - pad .. j - pad + k - 1] inside [0, n)
 // (padding never wins); average pooling adds the window's values left to right
 // (padding counts as 0) and divides by k.
+// Windows of up to kPoolUnroll: every neighbour is loaded first (indices clamped into
+// the row, out-of-window values replaced after the load), then reduced in window order.
+// A missing neighbour is -inf for the maximum, and +0 for the sum, which a running sum
+// started at +0 never turns negative-zero, so both match the loop below bit for bit.
+constexpr int kPoolUnroll = 8;
+__device__ __forceinline__ float pooled_unrolled(const float* c, int64_t n, int64_t j, int k,
+                                                 int mode) {
+  const int64_t lo = j - k / 2;
+  float v[kPoolUnroll];
+#pragma unroll
+  for (int t = 0; t < kPoolUnroll; ++t) {
+    const int64_t x = lo + t;
+    const float ld = c[x < 0 ? 0 : (x >= n ? n - 1 : x)];
+    v[t] = (t < k && x >= 0 && x < n) ? ld : (mode == 0 ? -INFINITY : 0.f);
+  }
+  if (mode == 0) {
+    float m = -INFINITY;
+    bool nan = false;
+#pragma unroll
+    for (int t = 0; t < kPoolUnroll; ++t) {
+      nan |= v[t] != v[t];
+      m = fmaxf(m, v[t]);
+    }
+    return nan ? __int_as_float(0x7fc00000) : m;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int t = 0; t < kPoolUnroll; ++t)
+    if (t < k) s = __fadd_rn(s, v[t]);
+  return __fdiv_rn(s, (float)k);
+}
+
 __device__ __forceinline__ float pooled(const float* c, int64_t n, int64_t j, int k, int mode) {
   if (k <= 1) return c[j];
+  if (k <= kPoolUnroll) return pooled_unrolled(c, n, j, k, mode);
   const int64_t lo = j - k / 2;
   if (mode == 0) {
     float m = -INFINITY;
