@@ -141,13 +141,13 @@ votes_kernel(AttnView a, int Hkv, int G, int64_t q_len, int64_t kv_len, int w,
 // A missing neighbour is -inf for the maximum, and +0 for the sum, which a running sum
 // started at +0 never turns negative-zero, so both match the loop below bit for bit.
 constexpr int kPoolUnroll = 8;
-__device__ __forceinline__ float pooled_unrolled(const float* c, int64_t n, int64_t j, int k,
-                                                 int mode) {
-  const int64_t lo = j - k / 2;
+template <typename I>
+__device__ __forceinline__ float pooled_unrolled(const float* c, I n, I j, int k, int mode) {
+  const I lo = j - k / 2;
   float v[kPoolUnroll];
 #pragma unroll
   for (int t = 0; t < kPoolUnroll; ++t) {
-    const int64_t x = lo + t;
+    const I x = lo + t;
     const float ld = c[x < 0 ? 0 : (x >= n ? n - 1 : x)];
     v[t] = (t < k && x >= 0 && x < n) ? ld : (mode == 0 ? -INFINITY : 0.f);
   }
@@ -168,15 +168,16 @@ __device__ __forceinline__ float pooled_unrolled(const float* c, int64_t n, int6
   return __fdiv_rn(s, (float)k);
 }
 
-__device__ __forceinline__ float pooled(const float* c, int64_t n, int64_t j, int k, int mode) {
+template <typename I>
+__device__ __forceinline__ float pooled(const float* c, I n, I j, int k, int mode) {
   if (k <= 1) return c[j];
-  if (k <= kPoolUnroll) return pooled_unrolled(c, n, j, k, mode);
-  const int64_t lo = j - k / 2;
+  if (k <= kPoolUnroll) return pooled_unrolled<I>(c, n, j, k, mode);
+  const I lo = j - k / 2;
   if (mode == 0) {
     float m = -INFINITY;
     bool nan = false;
     for (int t = 0; t < k; ++t) {
-      const int64_t x = lo + t;
+      const I x = lo + t;
       if (x < 0 || x >= n) continue;
       const float v = c[x];
       nan |= v != v;
@@ -186,7 +187,7 @@ __device__ __forceinline__ float pooled(const float* c, int64_t n, int64_t j, in
   }
   float s = 0.f;
   for (int t = 0; t < k; ++t) {
-    const int64_t x = lo + t;
+    const I x = lo + t;
     if (x >= 0 && x < n) s = __fadd_rn(s, c[x]);
   }
   return __fdiv_rn(s, (float)k);
@@ -218,23 +219,28 @@ __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* scra
 
 // Keys of the candidates: in LDS (staged once) when the row fits, else
 // recomputed from the votes in global memory on every pass.
+template <typename I>
 struct KeySource {
   const float* c;
-  int64_t n;
+  I n;
   int pool_k, pool_mode;
   const uint32_t* lds;   // n keys, or null
-  __device__ __forceinline__ uint32_t operator()(int64_t j) const {
-    return lds ? lds[j] : score_key(pooled(c, n, j, pool_k, pool_mode));
+  __device__ __forceinline__ uint32_t operator()(I j) const {
+    return lds ? lds[j] : score_key(pooled<I>(c, n, j, pool_k, pool_mode));
   }
 };
 
 // One workgroup per (b, kv): sink positions, then the select_k best pooled
 // candidates of [sink, recent_start) (ties: the earlier position), then the
-// recent positions, in ascending order.
+// recent positions, in ascending order.  I: the candidates' index type, int for rows
+// staged in LDS (at most kMaxStagedKeys candidates, 32-bit index arithmetic), int64_t
+// for longer rows, whose keys are recomputed from global memory on every pass.
+template <typename I>
 __global__ void __launch_bounds__(kPickThreads)
 select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int64_t recent_start,
               int64_t select_k, int pool_k, int pool_mode, int64_t* __restrict__ keep,
-              int64_t budget, int staged) {
+              int64_t budget) {
+  constexpr bool staged = sizeof(I) == 4;
   extern __shared__ uint32_t lds_keys[];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_prefix, s_mask, s_need;
@@ -242,32 +248,32 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const float* c = votes + row * kv_len + sink;
-  const int64_t n = recent_start - sink;
+  const I n = (I)(recent_start - sink);
   int64_t* out = keep + row * budget;
   for (int64_t i = tid; i < sink; i += kPickThreads) out[i] = i;
   for (int64_t i = tid; i < kv_len - recent_start; i += kPickThreads)
     out[sink + select_k + i] = recent_start + i;
   if (select_k <= 0) return;
-  KeySource key_of{c, n, pool_k, pool_mode, nullptr};
-  if (staged) {
+  KeySource<I> key_of{c, n, pool_k, pool_mode, nullptr};
+  if constexpr (staged) {
     // the row's votes into LDS (8 loads in flight per thread), then the keys
     float* raw = reinterpret_cast<float*>(lds_keys + n);
-    for (int64_t j0 = tid; j0 < n; j0 += 8 * kPickThreads) {
+    for (I j0 = tid; j0 < n; j0 += 8 * kPickThreads) {
       float x[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int64_t j = j0 + u * kPickThreads;
+        const I j = j0 + u * kPickThreads;
         x[u] = j < n ? c[j] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int64_t j = j0 + u * kPickThreads;
+        const I j = j0 + u * kPickThreads;
         if (j < n) raw[j] = x[u];
       }
     }
     __syncthreads();
-    for (int64_t j = tid; j < n; j += kPickThreads)
-      lds_keys[j] = score_key(pooled(raw, n, j, pool_k, pool_mode));
+    for (I j = tid; j < n; j += kPickThreads)
+      lds_keys[j] = score_key(pooled<I>(raw, n, j, pool_k, pool_mode));
     key_of.lds = lds_keys;
   }
   // radix select of the select_k-th largest key, 8 bits at a time from the top
@@ -281,7 +287,7 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
     if (tid < 256) hist[tid] = 0;
     __syncthreads();
     const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int64_t j = tid; j < n; j += kPickThreads) {
+    for (I j = tid; j < n; j += kPickThreads) {
       const uint32_t key = key_of(j);
       if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
     }
@@ -317,10 +323,10 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
   const int64_t take_equal = s_need;
   // each thread scans one contiguous range: counts, then a block scan of the
   // counts gives each thread its first output slot
-  const int64_t per = (n + kPickThreads - 1) / kPickThreads;
-  const int64_t j0 = min<int64_t>(n, tid * per), j1 = min<int64_t>(n, j0 + per);
+  const I per = (n + kPickThreads - 1) / kPickThreads;
+  const I j0 = min<I>(n, tid * per), j1 = min<I>(n, j0 + per);
   int64_t above = 0, equal = 0;
-  for (int64_t j = j0; j < j1; ++j) {
+  for (I j = j0; j < j1; ++j) {
     const uint32_t key = key_of(j);
     above += key > thr;
     equal += key == thr;
@@ -330,7 +336,7 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
   const int64_t eq_take = max<int64_t>(0, min<int64_t>(equal, take_equal - eq_before));
   int64_t slot = block_exclusive_scan(above + eq_take, s_count);
   int64_t eq_left = eq_take;
-  for (int64_t j = j0; j < j1; ++j) {
+  for (I j = j0; j < j1; ++j) {
     const uint32_t key = key_of(j);
     bool take = key > thr;
     if (key == thr && eq_left > 0) {
@@ -398,18 +404,23 @@ extern "C" int pk_select_prompt(const float* votes, int64_t rows, int64_t kv_len
     if (!votes || !keep) return pk::fail("null pointer");
     const int64_t budget = sink + select_k + (kv_len - recent_start);
     const int64_t n = recent_start - sink;
-    const int staged = n <= kMaxStagedKeys ? 1 : 0;
+    const bool staged = n <= kMaxStagedKeys;
     const size_t lds = staged ? (size_t)n * 8 : 0;
     static bool lds_opt_in = [] {
-      return hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel),
+      return hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel<int>),
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                  (int)(kMaxStagedKeys * 8)) == hipSuccess;
     }();
     if (staged && lds > 64 * 1024 && !lds_opt_in)
       return pk::fail("cannot reserve the selection kernel's LDS"), PK_ERR_RUNTIME;
-    hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(kPickThreads), lds,
-                       static_cast<hipStream_t>(stream), votes, kv_len, sink, recent_start,
-                       select_k, pool_kernel, pool_mode, keep, budget, staged);
+    if (staged)
+      hipLaunchKernelGGL(select_kernel<int>, dim3((unsigned)rows), dim3(kPickThreads), lds,
+                         static_cast<hipStream_t>(stream), votes, kv_len, sink, recent_start,
+                         select_k, pool_kernel, pool_mode, keep, budget);
+    else
+      hipLaunchKernelGGL(select_kernel<int64_t>, dim3((unsigned)rows), dim3(kPickThreads), 0,
+                         static_cast<hipStream_t>(stream), votes, kv_len, sink, recent_start,
+                         select_k, pool_kernel, pool_mode, keep, budget);
     return pk::check_launch("select_prompt");
   });
 }
