@@ -202,16 +202,17 @@ __device__ __forceinline__ uint32_t score_key(float v) {
 
 // Exclusive prefix sum of v over the workgroup's threads (tid order); uses
 // scratch[waves of the workgroup] and synchronizes the workgroup.
-__device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* scratch) {
+template <typename T>
+__device__ __forceinline__ T block_exclusive_scan(T v, T* scratch) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int64_t inc = v;
+  T inc = v;
   for (int o = 1; o < 64; o <<= 1) {
-    const int64_t u = __shfl_up(inc, o);
+    const T u = __shfl_up(inc, o);
     if (lane >= o) inc += u;
   }
   if (lane == 63) scratch[wave] = inc;
   __syncthreads();
-  int64_t before = 0;
+  T before = 0;
   for (int w = 0; w < wave; ++w) before += scratch[w];
   __syncthreads();
   return before + inc - v;
@@ -244,7 +245,7 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
   extern __shared__ uint32_t lds_keys[];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_prefix, s_mask, s_need;
-  __shared__ int64_t s_count[kPickThreads / 64];
+  __shared__ I s_count[kPickThreads / 64];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const float* c = votes + row * kv_len + sink;
@@ -320,22 +321,22 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
   }
   // the threshold key and how many candidates equal to it are kept (the earliest)
   const uint32_t thr = s_prefix;
-  const int64_t take_equal = s_need;
+  const I take_equal = (I)s_need;
   // each thread scans one contiguous range: counts, then a block scan of the
   // counts gives each thread its first output slot
   const I per = (n + kPickThreads - 1) / kPickThreads;
   const I j0 = min<I>(n, tid * per), j1 = min<I>(n, j0 + per);
-  int64_t above = 0, equal = 0;
+  I above = 0, equal = 0;
   for (I j = j0; j < j1; ++j) {
     const uint32_t key = key_of(j);
     above += key > thr;
     equal += key == thr;
   }
   // exclusive prefix of the equal counts decides which equal keys are taken
-  const int64_t eq_before = block_exclusive_scan(equal, s_count);
-  const int64_t eq_take = max<int64_t>(0, min<int64_t>(equal, take_equal - eq_before));
-  int64_t slot = block_exclusive_scan(above + eq_take, s_count);
-  int64_t eq_left = eq_take;
+  const I eq_before = block_exclusive_scan<I>(equal, s_count);
+  const I eq_take = max<I>(0, min<I>(equal, take_equal - eq_before));
+  I slot = block_exclusive_scan<I>(above + eq_take, s_count);
+  I eq_left = eq_take;
   for (I j = j0; j < j1; ++j) {
     const uint32_t key = key_of(j);
     bool take = key > thr;
@@ -343,7 +344,7 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
       take = true;
       --eq_left;
     }
-    if (take) out[sink + slot++] = sink + j;
+    if (take) out[sink + slot++] = sink + (int64_t)j;
   }
 }
 
