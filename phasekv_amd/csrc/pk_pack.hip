@@ -18,6 +18,9 @@
 namespace {
 
 constexpr int kThreads = 256;
+// Element counts below this run the fast pack kernels with 32-bit index arithmetic (no
+// 64-bit divisions per lane); larger tensors keep 64-bit indices.
+constexpr int64_t kIndex32 = int64_t(1) << 31;
 constexpr int kMaxDims = 8;
 
 // ---------------------------------------------------------------------------
@@ -222,19 +225,20 @@ __device__ __forceinline__ void store_quarter(uint8_t* dst, uint64_t x) {
 // Groups along the contiguous axis (V, per token along head_dim): a lane quad
 // per (row, group), the group index fastest; each lane one 16-byte load.
 // `block` / `nblocks`: this workgroup's place in the part of the grid doing this work.
-template <int BITS>
+template <int BITS, typename I>
 __device__ __forceinline__ void inner32_body(const uint16_t* __restrict__ x, int64_t rows,
                                              int64_t len, int64_t ngroups, int64_t nbytes,
                                              uint8_t* __restrict__ packed,
                                              uint16_t* __restrict__ scale,
                                              uint16_t* __restrict__ mins, int64_t block,
                                              int64_t nblocks) {
-  const int64_t total = rows * ngroups * 4;     // whole quads: every quad runs one iteration
-  for (int64_t i = block * blockDim.x + threadIdx.x; i < total; i += nblocks * blockDim.x) {
+  const I total = (I)(rows * ngroups * 4);     // whole quads: every quad runs one iteration
+  const I ng = (I)ngroups;
+  for (I i = (I)(block * blockDim.x + threadIdx.x); i < total; i += (I)(nblocks * blockDim.x)) {
     const int quarter = (int)(i & 3);
-    const int64_t j = i >> 2;
-    const int64_t r = j / ngroups, g = j - r * ngroups;
-    const pk_u4 q = *reinterpret_cast<const pk_u4*>(x + r * len + g * 32 + quarter * 8);
+    const I j = i >> 2;
+    const I r = j / ng, g = j - r * ng;
+    const pk_u4 q = *reinterpret_cast<const pk_u4*>(x + (r * (I)len + g * 32 + quarter * 8));
     float v[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -246,16 +250,16 @@ __device__ __forceinline__ void inner32_body(const uint16_t* __restrict__ x, int
       scale[j] = pk_f2h(st.scale);
       mins[j] = pk_f2h(st.mn);
     }
-    store_quarter<BITS>(packed + r * nbytes + g * 4 * BITS + quarter * BITS, pack8<BITS>(v, st));
+    store_quarter<BITS>(packed + (r * (I)nbytes + g * 4 * BITS + quarter * BITS), pack8<BITS>(v, st));
   }
 }
 
-template <int BITS>
+template <int BITS, typename I>
 __global__ void __launch_bounds__(kThreads)
 quantize_inner32_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t len, int64_t ngroups,
                         int64_t nbytes, uint8_t* __restrict__ packed, uint16_t* __restrict__ scale,
                         uint16_t* __restrict__ mins) {
-  inner32_body<BITS>(x, rows, len, ngroups, nbytes, packed, scale, mins, blockIdx.x, gridDim.x);
+  inner32_body<BITS, I>(x, rows, len, ngroups, nbytes, packed, scale, mins, blockIdx.x, gridDim.x);
 }
 
 // Groups along the second-innermost axis with a contiguous innermost dim D
@@ -263,23 +267,24 @@ quantize_inner32_kernel(const uint16_t* __restrict__ x, int64_t rows, int64_t le
 // quarter fastest, then the channel pair, so each load instruction of a wave
 // reads 64-byte runs of four token rows; each quad stores two channels' packed
 // group and metadata.
-template <int BITS>
+template <int BITS, typename I>
 __device__ __forceinline__ void outer32_body(const uint16_t* __restrict__ x, int64_t outer,
                                              int64_t len, int64_t D, int64_t ngroups,
                                              int64_t nbytes, uint8_t* __restrict__ packed,
                                              uint16_t* __restrict__ scale,
                                              uint16_t* __restrict__ mins, int meta_gm,
                                              int codes_tm, int64_t block, int64_t nblocks) {
-  const int64_t pairs = D / 2;
-  const int64_t total = outer * ngroups * pairs * 4;
-  for (int64_t i = block * blockDim.x + threadIdx.x; i < total; i += nblocks * blockDim.x) {
+  const I pairs = (I)(D / 2), ng = (I)ngroups, Di = (I)D;
+  const I total = (I)(outer * ngroups * (D / 2) * 4);
+  for (I i = (I)(block * blockDim.x + threadIdx.x); i < total; i += (I)(nblocks * blockDim.x)) {
     const int quarter = (int)(i & 3);
-    const int64_t rest = i >> 2;
-    const int64_t cp = rest % pairs;
-    const int64_t rest2 = rest / pairs;
-    const int64_t g = rest2 % ngroups, o = rest2 / ngroups;
+    const I rest = i >> 2;
+    const I rest2 = rest / pairs;
+    const I cp = rest - rest2 * pairs;
+    const I o = rest2 / ng;
+    const I g = rest2 - o * ng;
     const uint32_t* src =
-        reinterpret_cast<const uint32_t*>(x + (o * len + g * 32 + quarter * 8) * D + 2 * cp);
+        reinterpret_cast<const uint32_t*>(x + ((o * (I)len + g * 32 + quarter * 8) * Di + 2 * cp));
     float a[8], b[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
@@ -292,37 +297,37 @@ __device__ __forceinline__ void outer32_body(const uint16_t* __restrict__ x, int
     for (int k = 0; k < 2; ++k) {
       const float (&v)[8] = k ? b : a;
       const GroupStats st = quad_stats(v, quarter, BITS);
-      const int64_t row = o * D + 2 * cp + k;
+      const I row = o * Di + 2 * cp + k;
       if (quarter == 0) {
-        const int64_t mi = meta_gm ? (o * ngroups + g) * D + 2 * cp + k : row * ngroups + g;
+        const I mi = meta_gm ? (o * ng + g) * Di + 2 * cp + k : row * ng + g;
         scale[mi] = pk_f2h(st.scale);
         mins[mi] = pk_f2h(st.mn);
       }
       code[k] = pack8<BITS>(v, st);
       if (!codes_tm)
-        store_quarter<BITS>(packed + row * nbytes + g * 4 * BITS + quarter * BITS, code[k]);
+        store_quarter<BITS>(packed + (row * (I)nbytes + g * 4 * BITS + quarter * BITS), code[k]);
     }
     if (codes_tm) {
       // byte jj of the quarter for both channels: one 2-byte store into [bytes][D]
-      uint8_t* base = packed + (o * nbytes + g * 4 * BITS + quarter * BITS) * D + 2 * cp;
+      uint8_t* base = packed + ((o * (I)nbytes + g * 4 * BITS + quarter * BITS) * Di + 2 * cp);
 #pragma unroll
       for (int jj = 0; jj < BITS; ++jj) {
         const uint32_t lo = static_cast<uint32_t>(code[0] >> (8 * jj)) & 0xFFu;
         const uint32_t hi = static_cast<uint32_t>(code[1] >> (8 * jj)) & 0xFFu;
-        *reinterpret_cast<uint16_t*>(base + (int64_t)jj * D) = (uint16_t)(lo | (hi << 8));
+        *reinterpret_cast<uint16_t*>(base + jj * Di) = (uint16_t)(lo | (hi << 8));
       }
     }
   }
 }
 
-template <int BITS>
+template <int BITS, typename I>
 __global__ void __launch_bounds__(kThreads)
 quantize_outer32_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t len, int64_t D,
                         int64_t ngroups, int64_t nbytes, uint8_t* __restrict__ packed,
                         uint16_t* __restrict__ scale, uint16_t* __restrict__ mins, int meta_gm,
                         int codes_tm) {
-  outer32_body<BITS>(x, outer, len, D, ngroups, nbytes, packed, scale, mins, meta_gm, codes_tm,
-                     blockIdx.x, gridDim.x);
+  outer32_body<BITS, I>(x, outer, len, D, ngroups, nbytes, packed, scale, mins, meta_gm, codes_tm,
+                        blockIdx.x, gridDim.x);
 }
 
 // The cache's K/V block pack in one launch: workgroups [0, k_blocks) pack K
@@ -336,15 +341,15 @@ struct KVPackArgs {
   int k_blocks;
 };
 
-template <int BITS>
+template <int BITS, typename I>
 __global__ void __launch_bounds__(kThreads)
 quantize_kv32_kernel(const KVPackArgs a) {
   if ((int)blockIdx.x < a.k_blocks)
-    outer32_body<BITS>(a.k, a.outer, a.S, a.D, a.S / 32, a.S * BITS / 8, a.kp, a.ks, a.km, 1, 1,
-                       blockIdx.x, a.k_blocks);
+    outer32_body<BITS, I>(a.k, a.outer, a.S, a.D, a.S / 32, a.S * BITS / 8, a.kp, a.ks, a.km, 1,
+                          1, blockIdx.x, a.k_blocks);
   else
-    inner32_body<BITS>(a.v, a.outer * a.S, a.D, a.D / 32, a.D * BITS / 8, a.vp, a.vs, a.vm,
-                       blockIdx.x - a.k_blocks, gridDim.x - a.k_blocks);
+    inner32_body<BITS, I>(a.v, a.outer * a.S, a.D, a.D / 32, a.D * BITS / 8, a.vp, a.vs, a.vm,
+                          blockIdx.x - a.k_blocks, gridDim.x - a.k_blocks);
 }
 
 // General group sizes: metadata per (row, group) ...
@@ -532,10 +537,15 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
                       reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (fast && axis == ndim - 1 && !layout) {
       const int64_t lanes = p.rows * p.ngroups * 4;
-  #define PK_INNER(B) hipLaunchKernelGGL(quantize_inner32_kernel<B>, dim3(grid_for(lanes)), dim3(kThreads), \
-                                         0, s, static_cast<const uint16_t*>(x), p.rows, p.len, p.ngroups, \
-                                         p.nbytes, out_packed, out_scale, out_mins)
-      if (bits == 2) PK_INNER(2); else if (bits == 4) PK_INNER(4); else PK_INNER(8);
+      const bool i32 = p.rows * p.len < kIndex32;   // every element and byte index fits int
+  #define PK_INNER(B, I) hipLaunchKernelGGL((quantize_inner32_kernel<B, I>), dim3(grid_for(lanes)), \
+                                            dim3(kThreads), 0, s, static_cast<const uint16_t*>(x), p.rows, \
+                                            p.len, p.ngroups, p.nbytes, out_packed, out_scale, out_mins)
+      if (i32) {
+        if (bits == 2) PK_INNER(2, int); else if (bits == 4) PK_INNER(4, int); else PK_INNER(8, int);
+      } else {
+        if (bits == 2) PK_INNER(2, int64_t); else if (bits == 4) PK_INNER(4, int64_t); else PK_INNER(8, int64_t);
+      }
   #undef PK_INNER
       return pk::check_launch("quantize_pack");
     }
@@ -543,10 +553,16 @@ extern "C" int pk_quantize_pack(const void* x, int dtype, int ndim, const int64_
       const int64_t D = shape[ndim - 1];
       const int64_t outer = p.rows / D;
       const int64_t threads = outer * p.ngroups * (D / 2) * 4;
-  #define PK_OUTER(B) hipLaunchKernelGGL(quantize_outer32_kernel<B>, dim3(grid_for(threads)), dim3(kThreads), \
-                                         0, s, static_cast<const uint16_t*>(x), outer, p.len, D, p.ngroups, \
-                                         p.nbytes, out_packed, out_scale, out_mins, p.meta_gm, p.codes_tm)
-      if (bits == 2) PK_OUTER(2); else if (bits == 4) PK_OUTER(4); else PK_OUTER(8);
+      const bool i32 = p.rows * p.len < kIndex32;
+  #define PK_OUTER(B, I) hipLaunchKernelGGL((quantize_outer32_kernel<B, I>), dim3(grid_for(threads)), \
+                                            dim3(kThreads), 0, s, static_cast<const uint16_t*>(x), outer, \
+                                            p.len, D, p.ngroups, p.nbytes, out_packed, out_scale, out_mins, \
+                                            p.meta_gm, p.codes_tm)
+      if (i32) {
+        if (bits == 2) PK_OUTER(2, int); else if (bits == 4) PK_OUTER(4, int); else PK_OUTER(8, int);
+      } else {
+        if (bits == 2) PK_OUTER(2, int64_t); else if (bits == 4) PK_OUTER(4, int64_t); else PK_OUTER(8, int64_t);
+      }
   #undef PK_OUTER
       return pk::check_launch("quantize_pack");
     }
@@ -589,12 +605,22 @@ extern "C" int pk_quantize_pack_kv(const uint16_t* k, const uint16_t* v, int bat
     a.k_blocks = grid_for(k_lanes);
     const int grid = a.k_blocks + grid_for(v_lanes);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (bits == 2)
-      hipLaunchKernelGGL(quantize_kv32_kernel<2>, dim3(grid), dim3(kThreads), 0, s, a);
-    else if (bits == 4)
-      hipLaunchKernelGGL(quantize_kv32_kernel<4>, dim3(grid), dim3(kThreads), 0, s, a);
-    else
-      hipLaunchKernelGGL(quantize_kv32_kernel<8>, dim3(grid), dim3(kThreads), 0, s, a);
+    const bool i32 = a.outer * seq_len * head_dim < kIndex32;   // K and V indices fit int
+    if (i32) {
+      if (bits == 2)
+        hipLaunchKernelGGL((quantize_kv32_kernel<2, int>), dim3(grid), dim3(kThreads), 0, s, a);
+      else if (bits == 4)
+        hipLaunchKernelGGL((quantize_kv32_kernel<4, int>), dim3(grid), dim3(kThreads), 0, s, a);
+      else
+        hipLaunchKernelGGL((quantize_kv32_kernel<8, int>), dim3(grid), dim3(kThreads), 0, s, a);
+    } else {
+      if (bits == 2)
+        hipLaunchKernelGGL((quantize_kv32_kernel<2, int64_t>), dim3(grid), dim3(kThreads), 0, s, a);
+      else if (bits == 4)
+        hipLaunchKernelGGL((quantize_kv32_kernel<4, int64_t>), dim3(grid), dim3(kThreads), 0, s, a);
+      else
+        hipLaunchKernelGGL((quantize_kv32_kernel<8, int64_t>), dim3(grid), dim3(kThreads), 0, s, a);
+    }
     return pk::check_launch("quantize_pack_kv");
   });
 }
