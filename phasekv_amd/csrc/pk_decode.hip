@@ -1101,9 +1101,11 @@ static int launch_combine(const float* m, const float* l, const float* acc, int6
   // "0" workgroup slices, "1" rows, "2" waves: force a kernel where it applies, for experiments
   const char* force = getenv("PK_COMBINE_KERNEL");
   const int kind = (force && *force) ? atoi(force) : -1;
-  // one round trip per thread: few partials per row (measured on MI355X: 4.3 -> 2.9 us
-  // at 448 rows of 8, 25.5 -> 3 us at 7168 rows of 3; no gain at 896 rows of 10)
-  if (vec && (kind < 0 || kind == 1) && C <= kCombineLoads) {
+  // one round trip per thread: few partials per row over many rows (measured on MI355X:
+  // 4.3 -> 2.9 us at 448 rows of 8, 25.5 -> 3 us at 7168 rows of 3; no gain at 896 rows of
+  // 10); a few rows (C1: 14 of 5, 224 threads) go to the wave combine, 2.62 -> 2.45 us
+  const bool many_rows = rows * (hd / 4) >= 32 * kCombineRowsThreads;
+  if (vec && (kind == 1 || (kind < 0 && many_rows)) && C <= kCombineLoads) {
     const int64_t blocks = (rows * (hd / 4) + kCombineRowsThreads - 1) / kCombineRowsThreads;
     if (blocks > INT32_MAX) return fail("too many output rows");
     hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)blocks), dim3(kCombineRowsThreads), 0,

@@ -38,7 +38,7 @@ def _oracle(sets):
                                        (448, 8, 128), (448, 10, 128), (448, 16, 128),
                                        (280, 17, 128), (28, 35, 128), (28, 64, 64),
                                        (28, 65, 128), (14, 128, 64), (28, 150, 128),
-                                       (20, 40, 8)])
+                                       (20, 40, 8), (14, 5, 64), (28, 1, 128)])
 def test_merge_partials_matches_the_oracle(gpu, rows, n, hd):
     from phasekv_amd import decode as dec
     print(f"case rows={rows} n={n} hd={hd}", flush=True)
