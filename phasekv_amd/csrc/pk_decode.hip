@@ -197,8 +197,9 @@ decode_partials_generic(const DecodeParams p) {
 
 // Log-sum-exp merge of the C partials of each output row
 // (attention_triton.py:257-266, 300-307).  Three kernels share the contract; the
-// host picks by C (combine_rows_kernel for C <= 8, combine_wave_kernel for C <= 128,
-// this one for longer rows, head_dims below 16 and buffers not 16-byte aligned).
+// host picks by C and the row count (combine_rows_kernel for C <= 8 over many rows,
+// combine_wave_kernel for the other C <= 128, this one for longer rows, head_dims
+// below 16 and buffers not 16-byte aligned).
 // A workgroup owns one row and a slice of hs channels (16 <= hs <= 64, chosen by
 // the host from C: many partials per row give narrow slices, so a batch-1 decode
 // still spreads over rows * hd / 16 workgroups).  Thread (cs, d) owns channel d of partials cs, cs + ncs, ...
