@@ -344,10 +344,36 @@ combine_rows_kernel(const float* __restrict__ m, const float* __restrict__ l,
   }
 }
 
+// Sum / maximum over the 16 lanes of a wave that share lane & 3, all in the VALU:
+// DPP rotations by 8 and 4 within each 16-lane row, then permlane swaps across the
+// four rows (no trip through the LDS crossbar).
+__device__ __forceinline__ float dpp_ror(float v, int ctrl_sel) {
+  return ctrl_sel == 8
+             ? __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false))
+             : __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_column_sum(float v) {
+  v += dpp_ror(v, 8);
+  v += dpp_ror(v, 4);
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float quad_column_max(float v) {
+  v = fmaxf(v, dpp_ror(v, 8));
+  v = fmaxf(v, dpp_ror(v, 4));
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // The merge for few rows of more partials (8 < C <= 16 * NL: the batch-1 decodes,
 // 28 rows of 35 partials at C2).  One wave per (row, 16 channels): lane (cs, q)
 // holds channels 4q .. 4q + 3 of partials cs, cs + 16, ..., so the row maximum
-// and the sums are four lane exchanges, with no LDS and no barrier.
+// and the sums are two DPP rotations and two permlane swaps each, with no LDS and
+// no barrier.
 template <int NL>
 __global__ void __launch_bounds__(64)
 combine_wave_kernel(const float* __restrict__ m, const float* __restrict__ l,
@@ -377,7 +403,7 @@ combine_wave_kernel(const float* __restrict__ m, const float* __restrict__ l,
   float M = mk[0];
 #pragma unroll
   for (int k = 1; k < NL; ++k) M = fmaxf(M, mk[k]);
-  M = wave_max_over(M, 4);
+  M = quad_column_max(M);
   float4 S = make_float4(0, 0, 0, 0);
   float L = 0.f;
   if (M != -INFINITY) {
@@ -391,11 +417,11 @@ combine_wave_kernel(const float* __restrict__ m, const float* __restrict__ l,
       L += w * lk[k];
     }
   }
-  S.x = wave_sum_over(S.x, 4);
-  S.y = wave_sum_over(S.y, 4);
-  S.z = wave_sum_over(S.z, 4);
-  S.w = wave_sum_over(S.w, 4);
-  L = wave_sum_over(L, 4);
+  S.x = quad_column_sum(S.x);
+  S.y = quad_column_sum(S.y);
+  S.z = quad_column_sum(S.z);
+  S.w = quad_column_sum(S.w);
+  L = quad_column_sum(L);
   if (cs != 0) return;
   const int64_t o = row * hd + d;
   if (out) {
