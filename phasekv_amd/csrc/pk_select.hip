@@ -206,9 +206,23 @@ template <typename T>
 __device__ __forceinline__ T block_exclusive_scan(T v, T* scratch) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   T inc = v;
-  for (int o = 1; o < 64; o <<= 1) {
-    const T u = __shfl_up(inc, o);
-    if (lane >= o) inc += u;
+  if constexpr (sizeof(T) == 4) {
+    // 32-bit counts: DPP shifts away from lane 0 within each 16-lane row, then the
+    // earlier rows' totals (their last lanes), all in the VALU
+    inc += (T)__builtin_amdgcn_update_dpp(0, (int)inc, 0x111, 0xF, 0xF, false);
+    inc += (T)__builtin_amdgcn_update_dpp(0, (int)inc, 0x112, 0xF, 0xF, false);
+    inc += (T)__builtin_amdgcn_update_dpp(0, (int)inc, 0x114, 0xF, 0xF, false);
+    inc += (T)__builtin_amdgcn_update_dpp(0, (int)inc, 0x118, 0xF, 0xF, false);
+    const T t0 = (T)__builtin_amdgcn_readlane((int)inc, 15);
+    const T t1 = (T)__builtin_amdgcn_readlane((int)inc, 31);
+    const T t2 = (T)__builtin_amdgcn_readlane((int)inc, 47);
+    const int r = lane >> 4;
+    inc += (r > 0 ? t0 : 0) + (r > 1 ? t1 : 0) + (r > 2 ? t2 : 0);
+  } else {
+    for (int o = 1; o < 64; o <<= 1) {
+      const T u = __shfl_up(inc, o);
+      if (lane >= o) inc += u;
+    }
   }
   if (lane == 63) scratch[wave] = inc;
   __syncthreads();
@@ -299,9 +313,19 @@ select_kernel(const float* __restrict__ votes, int64_t kv_len, int64_t sink, int
     const uint32_t need = s_need;
     const bool digit = tid < 256;
     uint32_t suf = digit ? hist[tid] : 0u;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t v = __shfl_down(suf, o);
-      if ((tid & 63) + o < 64) suf += v;
+    // suffix sums within the wave, in the VALU: DPP shifts towards lane 0 within each
+    // 16-lane row (lanes past the row's end add 0), then every row adds the later
+    // rows' totals, read from their first lanes
+    suf += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)suf, 0x101, 0xF, 0xF, false);
+    suf += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)suf, 0x102, 0xF, 0xF, false);
+    suf += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)suf, 0x104, 0xF, 0xF, false);
+    suf += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)suf, 0x108, 0xF, 0xF, false);
+    {
+      const uint32_t t1 = __builtin_amdgcn_readlane(suf, 16);
+      const uint32_t t2 = __builtin_amdgcn_readlane(suf, 32);
+      const uint32_t t3 = __builtin_amdgcn_readlane(suf, 48);
+      const int r = (tid & 63) >> 4;
+      suf += (r < 1 ? t1 : 0u) + (r < 2 ? t2 : 0u) + (r < 3 ? t3 : 0u);
     }
     __syncthreads();
     if (digit) hist[tid] = suf;            // suffix within the wave
